@@ -1,0 +1,311 @@
+"""Python binding of the MI355X Roformer hot path (libmsst_hip.so, C ABI in
+include/msst_hip.h).
+
+This module is plumbing for tests and the benchmark: it loads the in-tree
+shared library with ctypes and passes torch device tensors to it as raw
+pointers on torch's current HIP stream.  There is no fallback: if the
+library is not built, `lib()` raises.
+
+The package directory name contains dashes, so it is loaded by path:
+
+    spec = importlib.util.spec_from_file_location(
+        "msst_amd", "<repo>/cuda-msst-infer_amd/__init__.py",
+        submodule_search_locations=["<repo>/cuda-msst-infer_amd"])
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libmsst_hip.so")
+
+F32, F16 = 0, 1
+ACT = {"none": 0, "gelu": 1, "sigmoid": 2, "silu": 3}
+
+_lib = None
+
+
+class MsstError(RuntimeError):
+    pass
+
+
+def build(jobs: int = 8) -> None:
+    """Compile the HIP kernels and the C ABI for gfx950 (hipcc)."""
+    subprocess.run(["make", "-s", f"-j{jobs}", "-C", PKG_DIR], check=True)
+
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f = ctypes.c_float
+
+
+class SeqLayout(ctypes.Structure):
+    _fields_ = [(n, _i64) for n in (
+        "n_outer", "n_inner", "seq_len", "tok_outer", "tok_inner", "tok_pos")]
+
+
+class LayerWeights(ctypes.Structure):
+    _fields_ = [(n, _vp) for n in (
+        "attn_gamma", "w_qkv", "w_gate", "b_gate", "w_out", "ff_gamma",
+        "w_ff1", "b_ff1", "w_ff2", "b_ff2", "final_gamma")]
+
+
+class StackDesc(ctypes.Structure):
+    _fields_ = [(n, _i64) for n in (
+        "batch", "frames", "bands", "dim", "heads", "dim_head", "ff_dim", "depth")] + [
+        ("w_dtype", _int)]
+
+
+_SIGS = {
+    "msst_abi_version": ([], _int),
+    "msst_status_string": ([_int], ctypes.c_char_p),
+    "msst_last_error": ([], ctypes.c_char_p),
+    "msst_linear": ([_vp, _int, _vp, _int, _vp, _vp, _vp, _int, _i64, _i64, _i64, _int, _vp], _int),
+    "msst_rms_norm": ([_vp, _int, _vp, _f, _vp, _int, _i64, _i64, _vp], _int),
+    "msst_rms_norm_gate": ([_vp, _int, _vp, _f, _vp, _int, _vp, _int, _vp, _vp, _i64, _i64,
+                            _int, _vp], _int),
+    "msst_rope_table": ([_int, _int, _vp, _vp], _int),
+    "msst_rope_table_device": ([_int, _int, _vp, _vp, _vp], _int),
+    "msst_rope_qk": ([_vp, _vp, _int, _vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
+    "msst_attention": ([_vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64, _f, _vp], _int),
+    "msst_gated_rope_attention": ([_vp, _int, _i64, _vp, _vp, _vp, _vp, _i64,
+                                   ctypes.POINTER(SeqLayout), _int, _int, _f, _vp], _int),
+    "msst_split_qkv_heads": ([_vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp], _int),
+    "msst_gate_merge_heads": ([_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _vp], _int),
+    "msst_cast": ([_vp, _int, _vp, _int, _i64, _vp], _int),
+    "msst_add": ([_vp, _vp, _vp, _int, _i64, _vp], _int),
+    "msst_swap_axes12": ([_vp, _vp, _int, _i64, _i64, _i64, _i64, _vp], _int),
+    "msst_roformer_stack_workspace": ([ctypes.POINTER(StackDesc)], _i64),
+    "msst_roformer_stack": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights), _vp,
+                             _vp, _i64, _vp], _int),
+    "msst_roformer_transformer": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights),
+                                   _int, _vp, _i64, _vp], _int),
+}
+
+EXPORTED = tuple(_SIGS)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MsstError(f"{LIB_PATH} is not built; run build() (hipcc, gfx950)")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGS.items():
+            fn = getattr(l, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = l
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        l = lib()
+        raise MsstError(f"{what}: {l.msst_status_string(rc).decode()} "
+                        f"({rc}): {l.msst_last_error().decode()}")
+
+
+# ---------------------------------------------------------------------------
+# torch helpers (torch is imported lazily: the C ABI itself needs no torch).
+# ---------------------------------------------------------------------------
+def _dt(t) -> int:
+    import torch
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.float16:
+        return F16
+    raise MsstError(f"unsupported dtype {t.dtype}")
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def linear(x, w, bias=None, act="none", residual=None, out=None, out_dtype=None):
+    """act(x . w^T + bias) (+ residual); returns `out` [.., N]."""
+    import torch
+    K = x.shape[-1]
+    N = w.shape[0]
+    M = x.numel() // K
+    if out is None:
+        od = out_dtype or (residual.dtype if residual is not None else torch.float32)
+        out = torch.empty(*x.shape[:-1], N, dtype=od, device=x.device)
+    check(lib().msst_linear(_ptr(x), _dt(x), _ptr(w), _dt(w), _ptr(bias), _ptr(residual),
+                            _ptr(out), _dt(out), M, K, N, ACT[act], _stream()), "msst_linear")
+    return out
+
+
+def rms_norm(x, gamma, scale, out=None, out_dtype=None):
+    import torch
+    D = x.shape[-1]
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
+    check(lib().msst_rms_norm(_ptr(x), _dt(x), _ptr(gamma), float(scale), _ptr(out), _dt(out),
+                              x.numel() // D, D, _stream()), "msst_rms_norm")
+    return out
+
+
+def rms_norm_gate(x, gamma, scale, w_gate, b_gate, out_dtype=None):
+    import torch
+    D = x.shape[-1]
+    rows = x.numel() // D
+    G = w_gate.shape[0]
+    out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
+    gates = torch.empty(*x.shape[:-1], G, dtype=torch.float32, device=x.device)
+    check(lib().msst_rms_norm_gate(_ptr(x), _dt(x), _ptr(gamma), float(scale), _ptr(out),
+                                   _dt(out), _ptr(w_gate), _dt(w_gate), _ptr(b_gate),
+                                   _ptr(gates), rows, D, G, _stream()), "msst_rms_norm_gate")
+    return out, gates
+
+
+def rope_table(n: int, dim_head: int):
+    import numpy as np
+    c = np.empty((n, dim_head // 2), np.float32)
+    s = np.empty((n, dim_head // 2), np.float32)
+    check(lib().msst_rope_table(n, dim_head, c.ctypes.data_as(_vp), s.ctypes.data_as(_vp)),
+          "msst_rope_table")
+    return c, s
+
+
+def rope_table_device(n: int, dim_head: int, device="cuda"):
+    import torch
+    c = torch.empty(n, dim_head // 2, dtype=torch.float32, device=device)
+    s = torch.empty_like(c)
+    check(lib().msst_rope_table_device(n, dim_head, _ptr(c), _ptr(s), _stream()),
+          "msst_rope_table_device")
+    return c, s
+
+
+def rope_qk_(q, k, cos_t, sin_t):
+    B, H, N, D = q.shape
+    check(lib().msst_rope_qk(_ptr(q), _ptr(k), _dt(q), _ptr(cos_t), _ptr(sin_t), B, H, N, D,
+                             _stream()), "msst_rope_qk")
+
+
+def attention(q, k, v, scale=0.0):
+    import torch
+    B, H, N, D = q.shape
+    Nk = k.shape[2]
+    out = torch.empty_like(q)
+    check(lib().msst_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _dt(q), B, H, N, Nk, D,
+                               float(scale), _stream()), "msst_attention")
+    return out
+
+
+def seq_layout(n_outer, n_inner, seq_len, tok_outer, tok_inner, tok_pos) -> SeqLayout:
+    return SeqLayout(n_outer, n_inner, seq_len, tok_outer, tok_inner, tok_pos)
+
+
+def gated_rope_attention(qkv, layout: SeqLayout, heads, cos_t=None, sin_t=None, gates=None,
+                         scale=0.0, out=None):
+    import torch
+    D = qkv.shape[-1] // (3 * heads)
+    tokens = qkv.numel() // qkv.shape[-1]
+    if out is None:
+        out = torch.empty(tokens, heads * D, dtype=qkv.dtype, device=qkv.device)
+    check(lib().msst_gated_rope_attention(_ptr(qkv), _dt(qkv), qkv.shape[-1], _ptr(cos_t),
+                                          _ptr(sin_t), _ptr(gates), _ptr(out), out.shape[-1],
+                                          ctypes.byref(layout), heads, D, float(scale),
+                                          _stream()), "msst_gated_rope_attention")
+    return out
+
+
+def split_qkv_heads(qkv, heads):
+    import torch
+    B, N, C = qkv.shape
+    D = C // (3 * heads)
+    q = torch.empty(B, heads, N, D, dtype=qkv.dtype, device=qkv.device)
+    k = torch.empty_like(q)
+    v = torch.empty_like(q)
+    check(lib().msst_split_qkv_heads(_ptr(qkv), _ptr(q), _ptr(k), _ptr(v), _dt(qkv), B, N, heads,
+                                     D, _stream()), "msst_split_qkv_heads")
+    return q, k, v
+
+
+def gate_merge_heads(attn, gates):
+    import torch
+    B, H, N, D = attn.shape
+    out = torch.empty(B, N, H * D, dtype=attn.dtype, device=attn.device)
+    check(lib().msst_gate_merge_heads(_ptr(attn), _ptr(gates), _ptr(out), _dt(attn), B, H, N, D,
+                                      _stream()), "msst_gate_merge_heads")
+    return out
+
+
+def cast(x, dtype):
+    import torch
+    out = torch.empty(x.shape, dtype=dtype, device=x.device)
+    check(lib().msst_cast(_ptr(x), _dt(x), _ptr(out), _dt(out), x.numel(), _stream()),
+          "msst_cast")
+    return out
+
+
+def add(a, b, out=None):
+    import torch
+    if out is None:
+        out = torch.empty_like(a)
+    check(lib().msst_add(_ptr(a), _ptr(b), _ptr(out), _dt(a), a.numel(), _stream()), "msst_add")
+    return out
+
+
+def swap_axes12(x):
+    """[A,P,Q,R] -> [A,Q,P,R] (new tensor)."""
+    import torch
+    A, P, Q, R = x.shape
+    out = torch.empty(A, Q, P, R, dtype=x.dtype, device=x.device)
+    check(lib().msst_swap_axes12(_ptr(x), _ptr(out), _dt(x), A, P, Q, R, _stream()),
+          "msst_swap_axes12")
+    return out
+
+
+class RoformerStack:
+    """Device-resident weights of an axial Roformer stack and its workspace.
+
+    layers: list of dicts (time0, freq0, time1, freq1, ...) holding torch
+    device tensors under the msst_layer_weights field names; matrices in the
+    stack dtype, gammas/biases fp32.  Mirrors the transformer part of
+    BSRoformer / MelBandRoformer (model_bs_roformer.cu:482-539).
+    """
+
+    def __init__(self, layers, final_gamma, batch, frames, bands, dim, heads, dim_head,
+                 ff_dim, w_dtype):
+        import torch
+        self.layers = layers
+        self.final_gamma = final_gamma
+        self.desc = StackDesc(batch, frames, bands, dim, heads, dim_head, ff_dim,
+                              len(layers) // 2, w_dtype)
+        ws = lib().msst_roformer_stack_workspace(ctypes.byref(self.desc))
+        if ws < 0:
+            check(-1, "msst_roformer_stack_workspace")
+        self.workspace = torch.empty(int(ws), dtype=torch.uint8, device="cuda")
+        arr = (LayerWeights * len(layers))()
+        for i, lw in enumerate(layers):
+            for name, _ in LayerWeights._fields_:
+                t = lw.get(name)
+                setattr(arr[i], name, None if t is None else t.data_ptr())
+        self._arr = arr
+
+    def __call__(self, x):
+        """In place on x [batch, frames, bands, dim] fp32 (device)."""
+        check(lib().msst_roformer_stack(_ptr(x), ctypes.byref(self.desc), self._arr,
+                                        _ptr(self.final_gamma), _ptr(self.workspace),
+                                        self.workspace.numel(), _stream()),
+              "msst_roformer_stack")
+        return x
+
+    def transformer(self, x, layer: int, axis: int):
+        """One transformer in place on x [batch, bands, frames, dim] fp32
+        (time-major); axis 0 = time, 1 = frequency."""
+        check(lib().msst_roformer_transformer(
+            _ptr(x), ctypes.byref(self.desc), ctypes.byref(self._arr[layer]), axis,
+            _ptr(self.workspace), self.workspace.numel(), _stream()),
+            "msst_roformer_transformer")
+        return x

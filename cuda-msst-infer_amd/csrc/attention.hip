@@ -1,0 +1,662 @@
+// attention.hip — flash attention for the Roformer layers (head dim 64).
+//
+// Replaces the materialised pipeline of ops_attention.cu:96-181 (QK^T GEMM,
+// fp32 score tensor, softmax kernel :390-452, PV GEMM) and, for the fused
+// Roformer path, the surrounding head split, RoPE, gate and head merge of
+// model_bs_roformer.cu:250-278 / model_mel_band_roformer.cu:34-163.  No
+// N x N score tensor is ever written: scores live in MFMA accumulators and
+// an online softmax (running max / running sum per query) folds each
+// 64-key block into the output.
+//
+// Per wave: 64 queries as two 32-query MFMA column blocks.
+//   S^T[key, q]  = K . Q^T     A = K from LDS, B = Q^T held in registers.
+//                              Each lane owns ONE query column, so the
+//                              per-query max and sum need only one
+//                              cross-lane step (lane ^ 32).
+//   O^T[d, q]   += V^T . P^T   A = V^T from LDS, B = P^T taken straight
+//                              from the S accumulator registers — P never
+//                              goes through LDS.  The rescale of O by
+//                              exp2(m_old - m_new) is per lane.
+// fp16 path: v_mfma_f32_32x32x16_f16.  The 8 keys a lane feeds per MFMA are
+// {4h..4h+3, 8+4h..8+4h+3} of a 16-key group (that is what the S
+// accumulator layout hands it); V^T is stored in LDS with key bits 2 and 3
+// swapped so those 8 keys are one aligned 16-byte read.
+// fp32 path: v_mfma_f32_32x32x2_f32, V in natural [key][d] layout (one key
+// per lane per MFMA, so no transpose is needed).
+//
+// Work split: HPW (heads per workgroup) = 1 for long sequences — the 4
+// waves take 4 consecutive 64-query tiles of one (sequence, head) and share
+// double-buffered K/V blocks; HPW = 4 for sequences of <= 64 positions —
+// each wave owns one head of the sequence.  Workgroup ids are dealt
+// XCD-aware (see gemm.hip) so the query tiles of one head share an L2.
+//
+// RoPE (ops_misc.cu:39-69, interleaved pairs) is applied in fp32 while Q and
+// K are staged; the gate (ops_fused.cu:285-303 output) multiplies the
+// normalised output in the epilogue, which writes merged rows
+// out[token, h*64 + d] directly.
+#include "msst_common.hpp"
+
+namespace msst {
+namespace {
+
+constexpr int kD = 64;
+constexpr int kKB = 64;  // keys per block
+
+struct AttnParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* out;
+    int64_t ld_in, ld_out;      // token row strides (elements)
+    int64_t head_in, head_out;  // element offset of head h within a row
+    const float* cos_t;         // [N, 32] or null
+    const float* sin_t;
+    const float* gates;         // [token, H] or null
+    int64_t n_inner;
+    int64_t q_outer, q_inner, q_pos;
+    int64_t k_outer, k_inner, k_pos;
+    int n_q, n_k;               // queries / keys per sequence
+    int H;
+    int qtiles;                 // 64*waves_per_head-query tiles per (seq, head)
+    int64_t total_items;        // workgroup work items
+    int per_xcd;
+    float scale_log2;           // softmax scale * log2(e)
+};
+
+__device__ __forceinline__ int64_t tok_q(const AttnParams& p, int64_t s, int64_t pos) {
+    return (s / p.n_inner) * p.q_outer + (s % p.n_inner) * p.q_inner + pos * p.q_pos;
+}
+__device__ __forceinline__ int64_t tok_k(const AttnParams& p, int64_t s, int64_t pos) {
+    return (s / p.n_inner) * p.k_outer + (s % p.n_inner) * p.k_inner + pos * p.k_pos;
+}
+
+// Rotate the 4 interleaved pairs held in x[0..7] (head dims 2i..2i+7,
+// pair index pi0 .. pi0+3) by the angles of position pos.
+__device__ __forceinline__ void rope8(float (&x)[8], const float* cos_t, const float* sin_t,
+                                      int pos, int pi0) {
+    f4 c = *reinterpret_cast<const f4*>(cos_t + pos * (kD / 2) + pi0);
+    f4 s = *reinterpret_cast<const f4*>(sin_t + pos * (kD / 2) + pi0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float a = x[2 * e], b = x[2 * e + 1];
+        x[2 * e] = a * c[e] - b * s[e];
+        x[2 * e + 1] = a * s[e] + b * c[e];
+    }
+}
+
+__device__ __forceinline__ int swap_bits23(int kr) {
+    return (kr & ~0xC) | ((kr & 4) << 1) | ((kr & 8) >> 1);
+}
+
+__device__ __forceinline__ void work_item(const AttnParams& p, int64_t& item) {
+    const int64_t b = blockIdx.x;
+    item = (b & 7) * (int64_t)p.per_xcd + (b >> 3);
+}
+
+// ===========================================================================
+// fp16
+// ===========================================================================
+template <int HPW>
+__global__ __launch_bounds__(256) void attn_f16_kernel(AttnParams p) {
+    constexpr int WPH = 4 / HPW;          // waves per head
+    constexpr int NSLOT = HPW == 1 ? 2 : 4;
+    constexpr int SLOT = 2 * kKB * kD;    // K block + V^T block (halves)
+    constexpr int GROUP = 256 / HPW;      // threads loading one head's block
+    constexpr int CH = kKB * 8 / GROUP;   // 16-byte chunks per thread per tensor
+    __shared__ __attribute__((aligned(16))) half_t lds[NSLOT * SLOT];
+
+    int64_t item;
+    work_item(p, item);
+    if (item >= p.total_items) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int head_local = w / WPH, qsub = w % WPH;
+    // item = (seq * head_groups + hg) * qtiles + qt
+    const int head_groups = (p.H + HPW - 1) / HPW;
+    const int qt_idx = (int)(item % p.qtiles);
+    const int64_t sh = item / p.qtiles;
+    const int hg = (int)(sh % head_groups);
+    const int64_t seq = sh / head_groups;
+    const int h = hg * HPW + head_local;
+    const bool head_ok = h < p.H;
+    const int q0 = (qt_idx * WPH + qsub) * 64;
+    const bool wave_active = head_ok && q0 < p.n_q;
+
+    const half_t* qb = reinterpret_cast<const half_t*>(p.q);
+    const half_t* kbp = reinterpret_cast<const half_t*>(p.k);
+    const half_t* vbp = reinterpret_cast<const half_t*>(p.v);
+
+    // ---- Q operand (B of S^T = K . Q^T), RoPE applied, held for the loop.
+    h8 qf[2][4];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + qt * 32 + lrow;
+        const bool ok = wave_active && qi < p.n_q;
+        const half_t* row = qb + (ok ? tok_q(p, seq, qi) * p.ld_in + h * p.head_in : 0);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int d0 = kk * 16 + lh * 8;
+            if (ok) {
+                h8 raw = *reinterpret_cast<const h8*>(row + d0);
+                if (p.cos_t) {
+                    float x[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] = (float)raw[e];
+                    rope8(x, p.cos_t, p.sin_t, qi, d0 / 2);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) raw[e] = (half_t)x[e];
+                }
+                qf[qt][kk] = raw;
+            } else {
+                qf[qt][kk] = h8{};
+            }
+        }
+    }
+
+    // ---- K/V block staging: this thread's group loads head h_load.
+    const int grp = tid / GROUP, gt = tid % GROUP;
+    const int h_load = hg * HPW + grp;
+    const bool load_ok = h_load < p.H;
+    h8 kreg[CH], vreg[CH];
+    auto load_block = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int chunk = gt + i * GROUP;  // 0..511
+            const int kr = chunk >> 3, c = chunk & 7;
+            const int key = kb * kKB + kr;
+            if (load_ok && key < p.n_k) {
+                const int64_t off = tok_k(p, seq, key) * p.ld_in + h_load * p.head_in + c * 8;
+                h8 kv = *reinterpret_cast<const h8*>(kbp + off);
+                if (p.cos_t) {
+                    float x[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[e] = (float)kv[e];
+                    rope8(x, p.cos_t, p.sin_t, key, c * 4);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) kv[e] = (half_t)x[e];
+                }
+                kreg[i] = kv;
+                vreg[i] = *reinterpret_cast<const h8*>(vbp + off);
+            } else {
+                kreg[i] = h8{};
+                vreg[i] = h8{};  // zero V rows: masked keys contribute 0 * 0
+            }
+        }
+    };
+    auto store_block = [&](int slot) {
+        half_t* Ks = lds + slot * SLOT;
+        half_t* Vt = Ks + kKB * kD;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int chunk = gt + i * GROUP;
+            const int kr = chunk >> 3, c = chunk & 7;
+            *reinterpret_cast<h8*>(Ks + kr * kD + ((c ^ (kr & 7)) << 3)) = kreg[i];
+            const int pos = swap_bits23(kr);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int d = c * 8 + e;
+                const int sw = (d ^ (d >> 3)) & 7;
+                Vt[d * kKB + ((((pos >> 3) ^ sw)) << 3) + (pos & 7)] = vreg[i][e];
+            }
+        }
+    };
+
+    f16x o[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) o[a][b] = f16x{};
+    float m_run[2] = {-INFINITY, -INFINITY};
+    float l_run[2] = {0.0f, 0.0f};
+
+    const int nkb = (p.n_k + kKB - 1) / kKB;
+    const int my_slot0 = HPW == 1 ? 0 : grp;
+    load_block(0);
+    store_block(my_slot0);
+    __syncthreads();
+
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int slot = HPW == 1 ? (kb & 1) : head_local;
+        if (HPW == 1 && kb + 1 < nkb) load_block(kb + 1);
+        if (wave_active) {
+            const half_t* Ks = lds + slot * SLOT;
+            const half_t* Vt = Ks + kKB * kD;
+            // S^T for the two 32-key halves and the two query blocks.
+            f16x s[2][2];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                s[k2][0] = f16x{};
+                s[k2][1] = f16x{};
+                const int kr = k2 * 32 + lrow;
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const int c = kk * 2 + lh;
+                    h8 kf = *reinterpret_cast<const h8*>(Ks + kr * kD + ((c ^ (kr & 7)) << 3));
+                    s[k2][0] = mfma32x32x16(kf, qf[0][kk], s[k2][0]);
+                    s[k2][1] = mfma32x32x16(kf, qf[1][kk], s[k2][1]);
+                }
+            }
+            const int key_base = kb * kKB;
+            const bool tail = key_base + kKB > p.n_k;
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        float x = s[k2][qt][v] * p.scale_log2;
+                        if (tail) {
+                            const int key = key_base + k2 * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                            if (key >= p.n_k) x = -INFINITY;
+                        }
+                        s[k2][qt][v] = x;
+                        mx = fmaxf(mx, x);
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float m_new = fmaxf(m_run[qt], mx);
+                const float alpha = exp2f(m_run[qt] - m_new);
+                m_run[qt] = m_new;
+                float psum = 0.0f;
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        float e = exp2f(s[k2][qt][v] - m_new);
+                        s[k2][qt][v] = e;
+                        psum += e;
+                    }
+                l_run[qt] = l_run[qt] * alpha + psum;
+#pragma unroll
+                for (int dm = 0; dm < 2; ++dm)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) o[qt][dm][v] *= alpha;
+            }
+            // O^T += V^T . P^T over 4 sixteen-key substeps.
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int k2 = t >> 1, tp = t & 1;
+                h8 pf[2];
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) pf[qt][e] = (half_t)s[k2][qt][8 * tp + e];
+                const int chunk = k2 * 4 + 2 * tp + lh;
+#pragma unroll
+                for (int dm = 0; dm < 2; ++dm) {
+                    const int d = dm * 32 + lrow;
+                    const int sw = (d ^ (d >> 3)) & 7;
+                    h8 vf = *reinterpret_cast<const h8*>(Vt + d * kKB + ((chunk ^ sw) << 3));
+                    o[0][dm] = mfma32x32x16(vf, pf[0], o[0][dm]);
+                    o[1][dm] = mfma32x32x16(vf, pf[1], o[1][dm]);
+                }
+            }
+        }
+        if (HPW == 1 && kb + 1 < nkb) store_block((kb + 1) & 1);
+        __syncthreads();
+    }
+
+    if (!wave_active) return;
+    half_t* ob = reinterpret_cast<half_t*>(p.out);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + qt * 32 + lrow;
+        const float l_tot = l_run[qt] + __shfl_xor(l_run[qt], 32, 64);
+        if (qi >= p.n_q) continue;
+        const int64_t tok = tok_q(p, seq, qi);
+        float scale = 1.0f / l_tot;
+        if (p.gates) scale *= p.gates[tok * p.H + h];
+        half_t* orow = ob + tok * p.ld_out + h * p.head_out;
+#pragma unroll
+        for (int dm = 0; dm < 2; ++dm)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = dm * 32 + 8 * g + 4 * lh;
+                h4 val;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) val[e] = (half_t)(o[qt][dm][4 * g + e] * scale);
+                *reinterpret_cast<h4*>(orow + d) = val;
+            }
+    }
+}
+
+// ===========================================================================
+// fp32
+// ===========================================================================
+template <int HPW>
+__global__ __launch_bounds__(256) void attn_f32_kernel(AttnParams p) {
+    constexpr int WPH = 4 / HPW;
+    constexpr int SLOT = 2 * kKB * kD;   // K block + V block (floats)
+    constexpr int GROUP = 256 / HPW;
+    constexpr int CH = kKB * 16 / GROUP;  // 16-byte chunks (4 floats) per thread
+    extern __shared__ __attribute__((aligned(16))) float lds_f[];
+
+    int64_t item;
+    work_item(p, item);
+    if (item >= p.total_items) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int head_local = w / WPH, qsub = w % WPH;
+    const int head_groups = (p.H + HPW - 1) / HPW;
+    const int qt_idx = (int)(item % p.qtiles);
+    const int64_t sh = item / p.qtiles;
+    const int hg = (int)(sh % head_groups);
+    const int64_t seq = sh / head_groups;
+    const int h = hg * HPW + head_local;
+    const bool head_ok = h < p.H;
+    const int q0 = (qt_idx * WPH + qsub) * 64;
+    const bool wave_active = head_ok && q0 < p.n_q;
+
+    const float* qb = reinterpret_cast<const float*>(p.q);
+    const float* kbp = reinterpret_cast<const float*>(p.k);
+    const float* vbp = reinterpret_cast<const float*>(p.v);
+
+    // Q operand: lane (query, half h) holds Q[q][32h .. 32h+31].
+    float qf[2][32];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + qt * 32 + lrow;
+        const bool ok = wave_active && qi < p.n_q;
+        const float* row = qb + (ok ? tok_q(p, seq, qi) * p.ld_in + h * p.head_in : 0);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float x[8];
+            if (ok) {
+                f4 a = *reinterpret_cast<const f4*>(row + 32 * lh + 8 * c);
+                f4 b = *reinterpret_cast<const f4*>(row + 32 * lh + 8 * c + 4);
+                x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
+                x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
+                if (p.cos_t) rope8(x, p.cos_t, p.sin_t, qi, 16 * lh + 4 * c);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[qt][8 * c + e] = x[e];
+        }
+    }
+
+    const int grp = tid / GROUP, gt = tid % GROUP;
+    const int h_load = hg * HPW + grp;
+    const bool load_ok = h_load < p.H;
+    f4 kreg[CH], vreg[CH];
+    auto load_block = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int chunk = gt + i * GROUP;  // 0..1023
+            const int kr = chunk >> 4, c = chunk & 15;
+            const int key = kb * kKB + kr;
+            if (load_ok && key < p.n_k) {
+                const int64_t off = tok_k(p, seq, key) * p.ld_in + h_load * p.head_in + c * 4;
+                f4 kv = *reinterpret_cast<const f4*>(kbp + off);
+                if (p.cos_t) {
+                    // dims 4c..4c+3 are the pairs 2c and 2c+1
+                    const float* ct = p.cos_t + key * (kD / 2) + c * 2;
+                    const float* st = p.sin_t + key * (kD / 2) + c * 2;
+                    const float c0 = ct[0], c1 = ct[1], s0 = st[0], s1 = st[1];
+                    float a0 = kv[0], b0 = kv[1], a1 = kv[2], b1 = kv[3];
+                    kv[0] = a0 * c0 - b0 * s0;
+                    kv[1] = a0 * s0 + b0 * c0;
+                    kv[2] = a1 * c1 - b1 * s1;
+                    kv[3] = a1 * s1 + b1 * c1;
+                }
+                kreg[i] = kv;
+                vreg[i] = *reinterpret_cast<const f4*>(vbp + off);
+            } else {
+                kreg[i] = f4{};
+                vreg[i] = f4{};
+            }
+        }
+    };
+    auto store_block = [&](int slot) {
+        float* Ks = lds_f + slot * SLOT;
+        float* Vs = Ks + kKB * kD;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int chunk = gt + i * GROUP;
+            const int kr = chunk >> 4, c = chunk & 15;
+            *reinterpret_cast<f4*>(Ks + kr * kD + ((c ^ (kr & 15)) << 2)) = kreg[i];
+            *reinterpret_cast<f4*>(Vs + kr * kD + (c << 2)) = vreg[i];
+        }
+    };
+
+    f16x o[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) o[a][b] = f16x{};
+    float m_run[2] = {-INFINITY, -INFINITY};
+    float l_run[2] = {0.0f, 0.0f};
+
+    const int nkb = (p.n_k + kKB - 1) / kKB;
+    load_block(0);
+    store_block(HPW == 1 ? 0 : grp);
+    __syncthreads();
+
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int slot = HPW == 1 ? (kb & 1) : head_local;
+        if (HPW == 1 && kb + 1 < nkb) load_block(kb + 1);
+        if (wave_active) {
+            const float* Ks = lds_f + slot * SLOT;
+            const float* Vs = Ks + kKB * kD;
+            f16x s[2][2];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                s[k2][0] = f16x{};
+                s[k2][1] = f16x{};
+                const int kr = k2 * 32 + lrow;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const int cc = 8 * lh + c;  // K dims 32h + 4c .. +3
+                    f4 kf = *reinterpret_cast<const f4*>(Ks + kr * kD + ((cc ^ (kr & 15)) << 2));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        s[k2][0] = mfma32x32x2f32(kf[e], qf[0][4 * c + e], s[k2][0]);
+                        s[k2][1] = mfma32x32x2f32(kf[e], qf[1][4 * c + e], s[k2][1]);
+                    }
+                }
+            }
+            const int key_base = kb * kKB;
+            const bool tail = key_base + kKB > p.n_k;
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        float x = s[k2][qt][v] * p.scale_log2;
+                        if (tail) {
+                            const int key = key_base + k2 * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                            if (key >= p.n_k) x = -INFINITY;
+                        }
+                        s[k2][qt][v] = x;
+                        mx = fmaxf(mx, x);
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float m_new = fmaxf(m_run[qt], mx);
+                const float alpha = exp2f(m_run[qt] - m_new);
+                m_run[qt] = m_new;
+                float psum = 0.0f;
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        float e = exp2f(s[k2][qt][v] - m_new);
+                        s[k2][qt][v] = e;
+                        psum += e;
+                    }
+                l_run[qt] = l_run[qt] * alpha + psum;
+#pragma unroll
+                for (int dm = 0; dm < 2; ++dm)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) o[qt][dm][v] *= alpha;
+            }
+            // O^T += V^T . P^T: substep v of key half k2 feeds key
+            // k2*32 + 8(v/4) + 4h + v%4, which is register v of S.
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int key = k2 * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+#pragma unroll
+                    for (int dm = 0; dm < 2; ++dm) {
+                        const float vf = Vs[key * kD + dm * 32 + lrow];
+                        o[0][dm] = mfma32x32x2f32(vf, s[k2][0][v], o[0][dm]);
+                        o[1][dm] = mfma32x32x2f32(vf, s[k2][1][v], o[1][dm]);
+                    }
+                }
+        }
+        if (HPW == 1 && kb + 1 < nkb) store_block((kb + 1) & 1);
+        __syncthreads();
+    }
+
+    if (!wave_active) return;
+    float* ob = reinterpret_cast<float*>(p.out);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + qt * 32 + lrow;
+        const float l_tot = l_run[qt] + __shfl_xor(l_run[qt], 32, 64);
+        if (qi >= p.n_q) continue;
+        const int64_t tok = tok_q(p, seq, qi);
+        float scale = 1.0f / l_tot;
+        if (p.gates) scale *= p.gates[tok * p.H + h];
+        float* orow = ob + tok * p.ld_out + h * p.head_out;
+#pragma unroll
+        for (int dm = 0; dm < 2; ++dm)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = dm * 32 + 8 * g + 4 * lh;
+                f4 val;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) val[e] = o[qt][dm][4 * g + e] * scale;
+                *reinterpret_cast<f4*>(orow + d) = val;
+            }
+    }
+}
+
+int launch_attention(AttnParams& p, int64_t n_seq, int dtype, hipStream_t s) {
+    const int hpw = p.n_q <= 64 && p.n_k <= 64 ? 4 : 1;
+    const int wph = 4 / hpw;
+    p.qtiles = (p.n_q + 64 * wph - 1) / (64 * wph);
+    const int64_t head_groups = (p.H + hpw - 1) / hpw;
+    p.total_items = n_seq * head_groups * p.qtiles;
+    p.per_xcd = (int)((p.total_items + 7) / 8);
+    const int64_t grid = (int64_t)p.per_xcd * 8;
+    if (grid > 0x7fffffff) return set_error(MSST_ERR_UNSUPPORTED, "attention grid too large");
+    if (dtype == MSST_F16) {
+        if (hpw == 4)
+            hipLaunchKernelGGL(attn_f16_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL(attn_f16_kernel<1>, dim3((unsigned)grid), dim3(256), 0, s, p);
+        return check_launch("attn_f16_kernel");
+    }
+    if (hpw == 4) {
+        const size_t lds = 4 * 2 * kKB * kD * sizeof(float);
+        hipLaunchKernelGGL(attn_f32_kernel<4>, dim3((unsigned)grid), dim3(256), lds, s, p);
+    } else {
+        const size_t lds = 2 * 2 * kKB * kD * sizeof(float);
+        hipLaunchKernelGGL(attn_f32_kernel<1>, dim3((unsigned)grid), dim3(256), lds, s, p);
+    }
+    return check_launch("attn_f32_kernel");
+}
+
+bool fp32_lds_configured = false;
+
+int configure_f32_lds() {
+    if (fp32_lds_configured) return MSST_OK;
+    // 128 KB of dynamic LDS for the 4-head fp32 variant (gfx950 has 160 KB).
+    hipError_t e1 = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_f32_kernel<4>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        4 * 2 * kKB * kD * (int)sizeof(float));
+    hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_f32_kernel<1>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        2 * 2 * kKB * kD * (int)sizeof(float));
+    if (e1 != hipSuccess || e2 != hipSuccess)
+        return set_error(MSST_ERR_LAUNCH, "hipFuncSetAttribute(MaxDynamicSharedMemorySize) failed");
+    fp32_lds_configured = true;
+    return MSST_OK;
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace
+}  // namespace msst
+
+extern "C" int msst_attention(const void* q, const void* k, const void* v, void* out, int dtype,
+                              int64_t B, int64_t H, int64_t N, int64_t Nk, int64_t D, float scale,
+                              void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(q && k && v && out, MSST_ERR_INVALID_ARG, "null tensor pointer");
+    MSST_REQUIRE(is_dtype(dtype), MSST_ERR_INVALID_ARG, "bad dtype");
+    MSST_REQUIRE(B >= 0 && H >= 0 && N >= 0 && Nk >= 0, MSST_ERR_INVALID_ARG, "bad shape");
+    MSST_REQUIRE(D == kD, MSST_ERR_UNSUPPORTED, "head dim must be 64");
+    MSST_REQUIRE(N < (1 << 30) && Nk < (1 << 30), MSST_ERR_UNSUPPORTED, "sequence too long");
+    MSST_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 16),
+                 MSST_ERR_ALIGNMENT, "q, k, v, out must be 16-byte aligned");
+    if (B * H == 0 || N == 0) return MSST_OK;
+    MSST_REQUIRE(Nk > 0, MSST_ERR_INVALID_ARG, "no keys");
+    if (dtype == MSST_F32) {
+        int rc = configure_f32_lds();
+        if (rc) return rc;
+    }
+    if (scale == 0.0f) scale = 1.0f / sqrtf((float)D);
+    AttnParams p{};
+    p.q = q; p.k = k; p.v = v; p.out = out;
+    p.ld_in = D; p.ld_out = D; p.head_in = 0; p.head_out = 0;
+    p.cos_t = nullptr; p.sin_t = nullptr; p.gates = nullptr;
+    p.n_inner = 1;
+    p.q_outer = N; p.q_inner = 0; p.q_pos = 1;
+    p.k_outer = Nk; p.k_inner = 0; p.k_pos = 1;
+    p.n_q = (int)N; p.n_k = (int)Nk; p.H = 1;
+    p.scale_log2 = scale * kLog2e;
+    return launch_attention(p, B * H, dtype, as_stream(stream));
+}
+
+extern "C" int msst_gated_rope_attention(const void* qkv, int dtype, int64_t ld_qkv,
+                                         const float* cos_t, const float* sin_t,
+                                         const float* gates, void* out, int64_t ld_out,
+                                         const msst_seq_layout* layout, int H, int D, float scale,
+                                         void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(qkv && out && layout, MSST_ERR_INVALID_ARG, "null pointer");
+    MSST_REQUIRE(is_dtype(dtype), MSST_ERR_INVALID_ARG, "bad dtype");
+    MSST_REQUIRE(D == kD, MSST_ERR_UNSUPPORTED, "head dim must be 64");
+    MSST_REQUIRE(H > 0 && ld_qkv >= 3LL * H * D && ld_out >= (int64_t)H * D,
+                 MSST_ERR_INVALID_ARG, "row strides too small for 3*H*D / H*D");
+    MSST_REQUIRE((cos_t == nullptr) == (sin_t == nullptr), MSST_ERR_INVALID_ARG,
+                 "cos and sin tables must both be given or both be null");
+    const msst_seq_layout& L = *layout;
+    MSST_REQUIRE(L.n_outer >= 0 && L.n_inner >= 1 && L.seq_len >= 0 && L.seq_len < (1 << 30),
+                 MSST_ERR_INVALID_ARG, "bad sequence layout");
+    const size_t eb = dtype_bytes(dtype);
+    MSST_REQUIRE(aligned(qkv, 16) && aligned(out, 16) && (ld_qkv * eb) % 16 == 0 &&
+                     (ld_out * eb) % 16 == 0 && aligned(cos_t, 16) && aligned(sin_t, 16) &&
+                     aligned(gates, 4),
+                 MSST_ERR_ALIGNMENT, "qkv/out rows and RoPE tables must be 16-byte aligned");
+    const int64_t n_seq = L.n_outer * L.n_inner;
+    if (n_seq == 0 || L.seq_len == 0) return MSST_OK;
+    if (dtype == MSST_F32) {
+        int rc = configure_f32_lds();
+        if (rc) return rc;
+    }
+    if (scale == 0.0f) scale = 1.0f / sqrtf((float)D);
+    AttnParams p{};
+    const char* base = reinterpret_cast<const char*>(qkv);
+    p.q = base;
+    p.k = base + (size_t)H * D * eb;
+    p.v = base + (size_t)2 * H * D * eb;
+    p.out = out;
+    p.ld_in = ld_qkv; p.ld_out = ld_out; p.head_in = D; p.head_out = D;
+    p.cos_t = cos_t; p.sin_t = sin_t; p.gates = gates;
+    p.n_inner = L.n_inner;
+    p.q_outer = p.k_outer = L.tok_outer;
+    p.q_inner = p.k_inner = L.tok_inner;
+    p.q_pos = p.k_pos = L.tok_pos;
+    p.n_q = p.n_k = (int)L.seq_len;
+    p.H = H;
+    p.scale_log2 = scale * kLog2e;
+    return launch_attention(p, n_seq, dtype, as_stream(stream));
+}

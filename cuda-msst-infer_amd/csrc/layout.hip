@@ -1,0 +1,209 @@
+// layout.hip — the layout and elementwise kernels the ops.h / Tensor layer
+// needs around the hot path (all HBM-bound, vectorised where aligned):
+//   msst_split_qkv_heads   [B,N,(3,H,D)] -> 3 x [B,H,N,D]
+//                          (model_mel_band_roformer.cu:34-74, :117-140)
+//   msst_gate_merge_heads  merged[b,n,h*D+d] = attn[b,h,n,d] * g[b,n,h]
+//                          (model_mel_band_roformer.cu:76-115, :142-163)
+//   msst_cast              f32 <-> f16 (tensor.cu:1269-1294)
+//   msst_add               elementwise add (tensor.cu:1365-1447)
+//   msst_swap_axes12       [A,P,Q,R] -> [A,Q,P,R], the permute({0,2,1,3})
+//                          .contiguous() of the depth loop
+//                          (model_bs_roformer.cu:491, :509; tensor.cu:868-903)
+// The fused Roformer stack does not use the first two: its attention kernel
+// reads the packed qkv rows and writes merged, gated rows directly.
+#include "msst_common.hpp"
+
+namespace msst {
+namespace {
+
+template <typename T>
+__global__ __launch_bounds__(256) void split_qkv_kernel(const T* __restrict__ qkv,
+                                                        T* __restrict__ q, T* __restrict__ k,
+                                                        T* __restrict__ v, int64_t total,
+                                                        int64_t N, int64_t H, int64_t D) {
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    // idx enumerates [B,H,N,D] outputs.
+    const int64_t d = idx % D;
+    const int64_t n = (idx / D) % N;
+    const int64_t h = (idx / (D * N)) % H;
+    const int64_t b = idx / (D * N * H);
+    const int64_t base = (b * N + n) * 3 * H * D + h * D + d;
+    q[idx] = qkv[base];
+    k[idx] = qkv[base + H * D];
+    v[idx] = qkv[base + 2 * H * D];
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void gate_merge_kernel(const T* __restrict__ attn,
+                                                         const float* __restrict__ gates,
+                                                         T* __restrict__ merged, int64_t total,
+                                                         int64_t N, int64_t H, int64_t D) {
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    // idx enumerates merged [B,N,H,D] outputs (coalesced writes).
+    const int64_t d = idx % D;
+    const int64_t h = (idx / D) % H;
+    const int64_t n = (idx / (D * H)) % N;
+    const int64_t b = idx / (D * H * N);
+    const float g = gates[(b * N + n) * H + h];
+    merged[idx] = (T)((float)attn[((b * H + h) * N + n) * D + d] * g);
+}
+
+template <typename S, typename D>
+__global__ __launch_bounds__(256) void cast_kernel(const S* __restrict__ src, D* __restrict__ dst,
+                                                   int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) dst[i] = (D)(float)src[i];
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void add_kernel(const T* a, const T* b, T* out, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) out[i] = (T)((float)a[i] + (float)b[i]);
+}
+
+// [A,P,Q,R] -> [A,Q,P,R]; one thread per 16-byte (or element) chunk of R.
+template <typename V>
+__global__ __launch_bounds__(256) void swap12_kernel(const V* __restrict__ src, V* __restrict__ dst,
+                                                     int64_t A, int64_t P, int64_t Q, int64_t R) {
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t total = A * P * Q * R;
+    for (; idx < total; idx += stride) {
+        // idx enumerates dst [A,Q,P,R] (coalesced writes)
+        const int64_t r = idx % R;
+        const int64_t pp = (idx / R) % P;
+        const int64_t qq = (idx / (R * P)) % Q;
+        const int64_t a = idx / (R * P * Q);
+        dst[idx] = src[((a * P + pp) * Q + qq) * R + r];
+    }
+}
+
+unsigned grid_for(int64_t n) {
+    int64_t g = (n + 255) / 256;
+    if (g > 65536) g = 65536;
+    return (unsigned)(g < 1 ? 1 : g);
+}
+
+}  // namespace
+}  // namespace msst
+
+extern "C" int msst_split_qkv_heads(const void* qkv, void* q, void* k, void* v, int dtype,
+                                    int64_t B, int64_t N, int64_t H, int64_t D, void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(qkv && q && k && v, MSST_ERR_INVALID_ARG, "null tensor pointer");
+    MSST_REQUIRE(is_dtype(dtype), MSST_ERR_INVALID_ARG, "bad dtype");
+    MSST_REQUIRE(B >= 0 && N >= 0 && H > 0 && D > 0, MSST_ERR_INVALID_ARG, "bad shape");
+    const int64_t total = B * H * N * D;
+    if (total == 0) return MSST_OK;
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = (unsigned)((total + 255) / 256);
+    if (dtype == MSST_F16)
+        hipLaunchKernelGGL(split_qkv_kernel<half_t>, dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const half_t*>(qkv), reinterpret_cast<half_t*>(q),
+                           reinterpret_cast<half_t*>(k), reinterpret_cast<half_t*>(v), total, N,
+                           H, D);
+    else
+        hipLaunchKernelGGL(split_qkv_kernel<float>, dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(qkv), reinterpret_cast<float*>(q),
+                           reinterpret_cast<float*>(k), reinterpret_cast<float*>(v), total, N, H,
+                           D);
+    return check_launch("split_qkv_kernel");
+}
+
+extern "C" int msst_gate_merge_heads(const void* attn, const float* gates, void* merged,
+                                     int dtype, int64_t B, int64_t H, int64_t N, int64_t D,
+                                     void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(attn && gates && merged, MSST_ERR_INVALID_ARG, "null tensor pointer");
+    MSST_REQUIRE(is_dtype(dtype), MSST_ERR_INVALID_ARG, "bad dtype");
+    MSST_REQUIRE(B >= 0 && N >= 0 && H > 0 && D > 0, MSST_ERR_INVALID_ARG, "bad shape");
+    const int64_t total = B * H * N * D;
+    if (total == 0) return MSST_OK;
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = (unsigned)((total + 255) / 256);
+    if (dtype == MSST_F16)
+        hipLaunchKernelGGL(gate_merge_kernel<half_t>, dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const half_t*>(attn), gates,
+                           reinterpret_cast<half_t*>(merged), total, N, H, D);
+    else
+        hipLaunchKernelGGL(gate_merge_kernel<float>, dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(attn), gates,
+                           reinterpret_cast<float*>(merged), total, N, H, D);
+    return check_launch("gate_merge_kernel");
+}
+
+extern "C" int msst_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,
+                         void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(src && dst, MSST_ERR_INVALID_ARG, "null tensor pointer");
+    MSST_REQUIRE(is_dtype(src_dtype) && is_dtype(dst_dtype), MSST_ERR_INVALID_ARG, "bad dtype");
+    MSST_REQUIRE(n >= 0, MSST_ERR_INVALID_ARG, "negative size");
+    if (n == 0) return MSST_OK;
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = grid_for(n);
+    if (src_dtype == MSST_F32 && dst_dtype == MSST_F16)
+        hipLaunchKernelGGL((cast_kernel<float, half_t>), dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(src), reinterpret_cast<half_t*>(dst), n);
+    else if (src_dtype == MSST_F16 && dst_dtype == MSST_F32)
+        hipLaunchKernelGGL((cast_kernel<half_t, float>), dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const half_t*>(src), reinterpret_cast<float*>(dst), n);
+    else if (src_dtype == MSST_F32)
+        hipLaunchKernelGGL((cast_kernel<float, float>), dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(src), reinterpret_cast<float*>(dst), n);
+    else
+        hipLaunchKernelGGL((cast_kernel<half_t, half_t>), dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const half_t*>(src), reinterpret_cast<half_t*>(dst), n);
+    return check_launch("cast_kernel");
+}
+
+extern "C" int msst_add(const void* a, const void* b, void* out, int dtype, int64_t n,
+                        void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(a && b && out, MSST_ERR_INVALID_ARG, "null tensor pointer");
+    MSST_REQUIRE(is_dtype(dtype), MSST_ERR_INVALID_ARG, "bad dtype");
+    MSST_REQUIRE(n >= 0, MSST_ERR_INVALID_ARG, "negative size");
+    if (n == 0) return MSST_OK;
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = grid_for(n);
+    if (dtype == MSST_F16)
+        hipLaunchKernelGGL(add_kernel<half_t>, dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const half_t*>(a), reinterpret_cast<const half_t*>(b),
+                           reinterpret_cast<half_t*>(out), n);
+    else
+        hipLaunchKernelGGL(add_kernel<float>, dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(a), reinterpret_cast<const float*>(b),
+                           reinterpret_cast<float*>(out), n);
+    return check_launch("add_kernel");
+}
+
+extern "C" int msst_swap_axes12(const void* src, void* dst, int dtype, int64_t A, int64_t P,
+                                int64_t Q, int64_t R, void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(src && dst && src != dst, MSST_ERR_INVALID_ARG,
+                 "null or aliased tensor pointer");
+    MSST_REQUIRE(is_dtype(dtype), MSST_ERR_INVALID_ARG, "bad dtype");
+    MSST_REQUIRE(A >= 0 && P >= 0 && Q >= 0 && R >= 0, MSST_ERR_INVALID_ARG, "bad shape");
+    const int64_t total = A * P * Q * R;
+    if (total == 0) return MSST_OK;
+    hipStream_t s = as_stream(stream);
+    const size_t rb = R * dtype_bytes(dtype);
+    if (rb % 16 == 0 && aligned(src, 16) && aligned(dst, 16)) {
+        const int64_t r16 = (int64_t)(rb / 16);
+        hipLaunchKernelGGL(swap12_kernel<u4>, dim3(grid_for(A * P * Q * r16)), dim3(256), 0, s,
+                           reinterpret_cast<const u4*>(src), reinterpret_cast<u4*>(dst), A, P, Q,
+                           r16);
+    } else if (dtype == MSST_F16) {
+        hipLaunchKernelGGL(swap12_kernel<half_t>, dim3(grid_for(total)), dim3(256), 0, s,
+                           reinterpret_cast<const half_t*>(src), reinterpret_cast<half_t*>(dst), A,
+                           P, Q, R);
+    } else {
+        hipLaunchKernelGGL(swap12_kernel<float>, dim3(grid_for(total)), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(src), reinterpret_cast<float*>(dst), A, P,
+                           Q, R);
+    }
+    return check_launch("swap12_kernel");
+}

@@ -1,0 +1,88 @@
+// msst_common.hpp — shared device types, MFMA wrappers, epilogue math and
+// the host-side status plumbing of the C ABI (include/msst_hip.h).
+//
+// Target: gfx950 only (wave64, v_mfma_f32_{32x32x16,16x16x32}_f16,
+// v_mfma_f32_{32x32x2,16x16x4}_f32, 160 KB LDS per CU).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "msst_hip.h"
+
+namespace msst {
+
+typedef _Float16 half_t;
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers.  Lane layouts (l = lane, h = l / 32 for 32-wide shapes):
+//   32x32x16 f16:  A lane holds A[l%32][8h .. 8h+7]; B lane holds
+//                  B[8h .. 8h+7][l%32]; D register v holds
+//                  D[8*(v/4) + 4h + v%4][l%32].
+//   32x32x2 f32:   A lane holds A[l%32][h]; B lane holds B[h][l%32];
+//                  D as above.
+// The K index handed to a lane only has to agree between A and B, so the
+// kernels map K positions to (lane half, register) however suits their LDS
+// layout.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f16x mfma32x32x16(h8 a, h8 b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f16x mfma32x32x2f32(float a, float b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Epilogue activations.  erff/expf are the ROCm device-library routines
+// (not fast-math approximations): the fp32 path is held to 1e-4.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float act_apply(float v, int act) {
+    if (act == MSST_ACT_GELU) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    if (act == MSST_ACT_SIGMOID) return 1.0f / (1.0f + expf(-v));
+    if (act == MSST_ACT_SILU) return v / (1.0f + expf(-v));
+    return v;
+}
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) { return (float)v; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) { return (T)v; }
+
+// Butterfly sum over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side status helpers.
+// ---------------------------------------------------------------------------
+int set_error(int code, const std::string& msg);
+int check_launch(const char* what);
+
+inline bool is_dtype(int dt) { return dt == MSST_F32 || dt == MSST_F16; }
+inline size_t dtype_bytes(int dt) { return dt == MSST_F16 ? 2 : 4; }
+inline bool aligned(const void* p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace msst
+
+#define MSST_REQUIRE(cond, code, msg)                                   \
+    do {                                                                \
+        if (!(cond)) return ::msst::set_error((code), std::string(__func__) + ": " + (msg)); \
+    } while (0)

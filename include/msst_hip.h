@@ -1,0 +1,214 @@
+/*
+ * msst_hip.h — C ABI of the MI355X (gfx950) Roformer hot path.
+ *
+ * This is the thin launcher layer beneath the C++ `cudasep::ops` / `Tensor`
+ * API (cuda-msst-infer_amd/host/ops.h), which keeps the reference's
+ * signatures.  Every entry point here:
+ *   - takes raw device pointers, element counts and an explicit stream
+ *     (`stream` is a hipStream_t; NULL means the null stream);
+ *   - validates shapes, dtypes and alignment on the host BEFORE launching and
+ *     returns MSST_OK (0) or a negative MSST_ERR_* code (message available
+ *     through msst_last_error(), thread-local);
+ *   - allocates nothing (the Roformer stack entry takes a caller workspace);
+ *   - throws nothing.
+ * Kernels are hand-written HIP for gfx950 (MFMA f16/f32, LDS-staged tiles);
+ * no BLAS library is called.
+ *
+ * Reference interfaces replaced (CUDA-MSST-Infer, src/):
+ *   msst_linear                 ops.h:65-66, :128-135  (ops_linear.cu:150-427,
+ *                               ops_fused.cu:203-303, :341-358)
+ *   msst_rms_norm               ops.h:56               (ops_norm.cu:455-491)
+ *   msst_rms_norm_gate          ops.h:56 + :134 fused  (rms_norm followed by
+ *                               linear_sigmoid, model_bs_roformer.cu:243, :268)
+ *   msst_rope_table(_device)    model_bs_roformer.cu:205-230
+ *   msst_rope_qk                ops.h:99-100           (ops_misc.cu:73-131)
+ *   msst_attention              ops.h:83-85            (ops_attention.cu:522-599)
+ *   msst_gated_rope_attention   model_bs_roformer.cu:250-278 (split heads,
+ *                               RoPE, attention, gate, merge fused)
+ *   msst_split_qkv_heads        model_mel_band_roformer.cu:34-74, :117-140
+ *   msst_gate_merge_heads       model_mel_band_roformer.cu:76-115, :142-163
+ *   msst_cast                   tensor.cu:1269-1294 (to_dtype)
+ *   msst_add                    tensor.cu:1365-1447 (operator+, add_)
+ *   msst_swap_axes12            tensor.cu:868-903 (permute + contiguous)
+ *   msst_roformer_stack         model_bs_roformer.cu:482-539,
+ *                               model_mel_band_roformer.cu:843-906
+ *   msst_roformer_transformer   model_bs_roformer.cu:310-331,
+ *                               model_mel_band_roformer.cu:621-651
+ */
+#ifndef MSST_HIP_H
+#define MSST_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define MSST_OK 0
+#define MSST_ERR_INVALID_ARG (-1)   /* null pointer, bad shape or dtype   */
+#define MSST_ERR_UNSUPPORTED (-2)   /* shape/dtype combination not built  */
+#define MSST_ERR_ALIGNMENT (-3)     /* pointer not aligned as required    */
+#define MSST_ERR_LAUNCH (-4)        /* hipLaunch / runtime error          */
+#define MSST_ERR_WORKSPACE (-5)     /* workspace too small                */
+
+/* Element types: same values as cudasep::DType (tensor.h:15). */
+#define MSST_F32 0
+#define MSST_F16 1
+
+/* Epilogue activations (ops_fused.cu:21-32). */
+#define MSST_ACT_NONE 0
+#define MSST_ACT_GELU 1    /* exact erf GELU */
+#define MSST_ACT_SIGMOID 2
+#define MSST_ACT_SILU 3
+
+int msst_abi_version(void);
+const char* msst_status_string(int status);
+const char* msst_last_error(void);
+
+/* out[M,N] = act(x[M,K] . W[N,K]^T + bias[N]) (+ residual[M,N]).
+ * W is nn.Linear layout [out,in], row-major.  The compute precision follows
+ * W's dtype as in the reference (ops_linear.cu:154): f16 W -> fp16 MFMA with
+ * fp32 accumulation, f32 W -> fp32 MFMA.  x may be f32 or f16 (converted to
+ * W's dtype as it is loaded).  bias (fp32) and residual (out_dtype) may be
+ * NULL; residual may alias out.  out_dtype is f32 or f16. */
+int msst_linear(const void* x, int x_dtype, const void* w, int w_dtype,
+                const float* bias, const void* residual, void* out, int out_dtype,
+                int64_t M, int64_t K, int64_t N, int act, void* stream);
+
+/* y = x * rsqrt(sum(x^2) + 1e-12) * gamma * scale per row of D elements. */
+int msst_rms_norm(const void* x, int x_dtype, const float* gamma, float scale,
+                  void* out, int out_dtype, int64_t rows, int64_t D,
+                  void* stream);
+
+/* msst_rms_norm, and in the same pass the attention gates
+ * gates[r, g] = sigmoid(sum_d y_r[d] * w_gate[g, d] + b_gate[g]) for
+ * g < G (G <= 16), computed from y rounded to out_dtype (what the
+ * reference's linear_sigmoid would read).  w_gate [G, D] is f32 or f16. */
+int msst_rms_norm_gate(const void* x, int x_dtype, const float* gamma,
+                       float scale, void* out, int out_dtype,
+                       const void* w_gate, int w_dtype, const float* b_gate,
+                       float* gates, int64_t rows, int64_t D, int G,
+                       void* stream);
+
+/* Host-side RoPE table, [n, dim_head/2] each (model_bs_roformer.cu:205-230). */
+int msst_rope_table(int n, int dim_head, float* cos_out, float* sin_out);
+
+/* The same table computed on the device into device buffers (same float
+ * formula; the device cosf/sinf may differ from the host's by an ulp). */
+int msst_rope_table_device(int n, int dim_head, float* cos_out, float* sin_out,
+                           void* stream);
+
+/* In-place interleaved RoPE on q, k [B,H,N,D] (dtype f32 or f16); cos/sin
+ * are fp32 device tables [N, D/2]. */
+int msst_rope_qk(void* q, void* k, int dtype, const float* cos_t,
+                 const float* sin_t, int64_t B, int64_t H, int64_t N, int64_t D,
+                 void* stream);
+
+/* out = softmax(scale * q.k^T) . v on contiguous [B,H,N,D] tensors
+ * (k, v: [B,H,Nk,D]); dtype f32 (fp32 MFMA) or f16 (fp16 MFMA, fp32
+ * softmax/accumulation).  scale == 0 means 1/sqrt(D).  D must be 64. */
+int msst_attention(const void* q, const void* k, const void* v, void* out,
+                   int dtype, int64_t B, int64_t H, int64_t N, int64_t Nk,
+                   int64_t D, float scale, void* stream);
+
+/* Token addressing of a batch of sequences inside a token-major buffer.
+ * Sequence s = so * n_inner + si (so < n_outer, si < n_inner); position p of
+ * it is token  so * tok_outer + si * tok_inner + p * tok_pos.
+ *   time axis over [B,F,T] tokens:  n_outer=B*F n_inner=1 len=T
+ *                                    tok_outer=T tok_inner=0 tok_pos=1
+ *   freq axis over [B,F,T] tokens:  n_outer=B n_inner=T len=F
+ *                                    tok_outer=F*T tok_inner=1 tok_pos=T */
+typedef struct {
+    int64_t n_outer, n_inner, seq_len;
+    int64_t tok_outer, tok_inner, tok_pos;
+} msst_seq_layout;
+
+/* The Roformer attention block after the QKV projection, fused:
+ * qkv rows [tokens, 3*H*D] (layout (qkv,h,d), row stride ld_qkv elements) ->
+ * RoPE(q,k) over the sequence positions -> softmax(scale q.k^T) v ->
+ * times gates[token*H + h] (NULL = 1) -> out[token, h*D + d] (row stride
+ * ld_out).  cos/sin (NULL = no RoPE) are [seq_len, D/2] fp32.  dtype is the
+ * element type of qkv and out.  D must be 64. */
+int msst_gated_rope_attention(const void* qkv, int dtype, int64_t ld_qkv,
+                              const float* cos_t, const float* sin_t,
+                              const float* gates, void* out, int64_t ld_out,
+                              const msst_seq_layout* layout, int H, int D,
+                              float scale, void* stream);
+
+/* [B,N,(3,H,D)] -> q,k,v [B,H,N,D] (same dtype). */
+int msst_split_qkv_heads(const void* qkv, void* q, void* k, void* v, int dtype,
+                         int64_t B, int64_t N, int64_t H, int64_t D,
+                         void* stream);
+
+/* merged[b,n,h*D+d] = attn[b,h,n,d] * gates[b,n,h]  (gates fp32). */
+int msst_gate_merge_heads(const void* attn, const float* gates, void* merged,
+                          int dtype, int64_t B, int64_t H, int64_t N, int64_t D,
+                          void* stream);
+
+/* Elementwise dtype conversion of n elements. */
+int msst_cast(const void* src, int src_dtype, void* dst, int dst_dtype,
+              int64_t n, void* stream);
+
+/* out[i] = a[i] + b[i] (all of one dtype; out may alias a or b). */
+int msst_add(const void* a, const void* b, void* out, int dtype, int64_t n,
+             void* stream);
+
+/* dst[A,Q,P,R] = src[A,P,Q,R]: the permute({0,2,1,3}).contiguous() of the
+ * depth loop (model_bs_roformer.cu:491, :509).  src and dst must differ. */
+int msst_swap_axes12(const void* src, void* dst, int dtype, int64_t A,
+                     int64_t P, int64_t Q, int64_t R, void* stream);
+
+/* Weights of one transformer (attention + feed-forward), as the Roformer
+ * models hold them (model_bs_roformer.h:78-98).  Matrices are [out,in] in
+ * the stack's weight dtype; gammas and biases are fp32.  final_gamma is the
+ * MelBandRoformer per-transformer output norm (NULL for BSRoformer). */
+typedef struct {
+    const float* attn_gamma; /* [dim]         */
+    const void* w_qkv;       /* [3*H*Dh, dim] */
+    const void* w_gate;      /* [H, dim]      */
+    const float* b_gate;     /* [H]           */
+    const void* w_out;       /* [dim, H*Dh]   */
+    const float* ff_gamma;   /* [dim]         */
+    const void* w_ff1;       /* [ff, dim]     */
+    const float* b_ff1;      /* [ff]          */
+    const void* w_ff2;       /* [dim, ff]     */
+    const float* b_ff2;      /* [dim]         */
+    const float* final_gamma;/* [dim] or NULL */
+} msst_layer_weights;
+
+typedef struct {
+    int64_t batch, frames, bands, dim, heads, dim_head, ff_dim, depth;
+    int w_dtype; /* MSST_F16: fp16 weights/activations, fp32 residual and
+                    accumulation; MSST_F32: fp32 throughout */
+} msst_stack_desc;
+
+/* Bytes of device workspace msst_roformer_stack needs for `desc`. */
+int64_t msst_roformer_stack_workspace(const msst_stack_desc* desc);
+
+/* The axial Roformer transformer stack, in place on the fp32 activation
+ * x [batch, frames, bands, dim] (the layout the reference's depth loop
+ * receives after band split).  layers holds 2*depth entries: time0, freq0,
+ * time1, freq1, ...  final_gamma (BSRoformer's final norm) may be NULL.
+ * workspace must hold msst_roformer_stack_workspace(desc) bytes, 256-byte
+ * aligned.  No allocation, no host synchronisation. */
+int msst_roformer_stack(float* x, const msst_stack_desc* desc,
+                        const msst_layer_weights* layers,
+                        const float* final_gamma, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
+/* One transformer (apply_transformer with depth 1, model_bs_roformer.cu:
+ * 310-331 / model_mel_band_roformer.cu:621-651) in place on the fp32
+ * activation x in time-major token order [batch, bands, frames, dim]:
+ * axis 0 attends over frames (the time layer), axis 1 over bands.  Same
+ * workspace as msst_roformer_stack (desc.depth is ignored). */
+int msst_roformer_transformer(float* x, const msst_stack_desc* desc,
+                              const msst_layer_weights* w, int axis,
+                              void* workspace, int64_t workspace_bytes,
+                              void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MSST_HIP_H */

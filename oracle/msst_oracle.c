@@ -1,0 +1,329 @@
+/*
+ * msst_oracle.c — CPU fp32 restatement of the Roformer transformer hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (parity checker + timed CPU baseline); the
+ * product never links it.  See msst_oracle.h for the per-function reference
+ * citations and the deliberate departures (true fp32 instead of TF32,
+ * precise libm instead of fast-math intrinsics).
+ *
+ * Parallelism: OpenMP over independent rows / (batch, head) pairs.  The GEMM
+ * packs W into 16-column panels and runs a 6x16 register micro-tile written
+ * with GCC vector extensions (AVX2 + FMA at -march=x86-64-v3).
+ */
+#include "msst_oracle.h"
+
+#include <math.h>
+#include <omp.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef float v8f __attribute__((vector_size(32), aligned(4)));
+
+#define MR 6
+#define NR 16
+
+int orc_num_threads(void) { return omp_get_max_threads(); }
+void orc_set_num_threads(int n) {
+    if (n > 0) omp_set_num_threads(n);
+}
+
+/* ops_fused.cu:21-24 (exact-erf GELU), :30-32 (sigmoid), :26-28 (SiLU). */
+static inline float act_apply(float v, int act) {
+    switch (act) {
+    case ORC_ACT_GELU:
+        return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    case ORC_ACT_SIGMOID:
+        return 1.0f / (1.0f + expf(-v));
+    case ORC_ACT_SILU:
+        return v / (1.0f + expf(-v));
+    default:
+        return v;
+    }
+}
+
+void orc_activation(const float* x, float* out, int64_t n, int act) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) out[i] = act_apply(x[i], act);
+}
+
+/* Pack W [N,K] (row-major) into panels of NR columns: panel p holds
+ * Wp[p][k][c] = W[p*NR + c][k], zero beyond N. */
+static float* pack_w(const float* w, int64_t K, int64_t N) {
+    int64_t np = (N + NR - 1) / NR;
+    float* wp = (float*)aligned_alloc(64, (size_t)(np * K * NR * sizeof(float) + 64));
+#pragma omp parallel for schedule(static)
+    for (int64_t p = 0; p < np; ++p) {
+        float* dst = wp + p * K * NR;
+        for (int64_t k = 0; k < K; ++k)
+            for (int c = 0; c < NR; ++c) {
+                int64_t n = p * NR + c;
+                dst[k * NR + c] = n < N ? w[n * K + k] : 0.0f;
+            }
+    }
+    return wp;
+}
+
+/* Reference semantics: cuBLAS C = X.W^T (ops_linear.cu:176-185, :318-326),
+ * then the bias kernel (ops_linear.cu:128-135) or the fused bias+activation
+ * kernel (ops_fused.cu:40-102).  The optional residual is the caller's
+ * `out + attn_out` (model_bs_roformer.cu:322, :326) folded in. */
+void orc_linear(const float* x, const float* w, const float* b,
+                const float* residual, float* out,
+                int64_t M, int64_t K, int64_t N, int act) {
+    if (M <= 0 || N <= 0) return;
+    float* wp = pack_w(w, K, N);
+    int64_t np = (N + NR - 1) / NR;
+    int64_t mb = (M + MR - 1) / MR;
+#pragma omp parallel for schedule(dynamic, 4)
+    for (int64_t ib = 0; ib < mb; ++ib) {
+        int64_t i0 = ib * MR;
+        int rows = (int)((M - i0) < MR ? (M - i0) : MR);
+        const float* arow[MR];
+        for (int r = 0; r < MR; ++r) arow[r] = x + (i0 + (r < rows ? r : 0)) * K;
+        for (int64_t p = 0; p < np; ++p) {
+            const float* panel = wp + p * K * NR;
+            v8f acc[MR][2];
+            memset(acc, 0, sizeof(acc));
+            for (int64_t k = 0; k < K; ++k) {
+                v8f w0 = *(const v8f*)(panel + k * NR);
+                v8f w1 = *(const v8f*)(panel + k * NR + 8);
+                for (int r = 0; r < MR; ++r) {
+                    float a = arow[r][k];
+                    acc[r][0] += a * w0;
+                    acc[r][1] += a * w1;
+                }
+            }
+            for (int r = 0; r < rows; ++r) {
+                int64_t i = i0 + r;
+                for (int c = 0; c < NR; ++c) {
+                    int64_t n = p * NR + c;
+                    if (n >= N) break;
+                    float v = acc[r][c >> 3][c & 7];
+                    if (b) v += b[n];
+                    v = act_apply(v, act);
+                    if (residual) v += residual[i * N + n];
+                    out[i * N + n] = v;
+                }
+            }
+        }
+    }
+    free(wp);
+}
+
+/* ops_norm.cu:85-111: sum of squares over the row, rsqrt(ss + 1e-12),
+ * times gamma and the caller's scale (sqrt(dim) at model_bs_roformer.cu:243). */
+void orc_rms_norm(const float* x, const float* gamma, float scale, float* out,
+                  int64_t rows, int64_t D) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xi = x + r * D;
+        float* yi = out + r * D;
+        double ss = 0.0; /* summed in double: the oracle's ss has no
+                            order-dependent rounding */
+        for (int64_t j = 0; j < D; ++j) ss += (double)xi[j] * (double)xi[j];
+        float inv = 1.0f / sqrtf((float)ss + 1e-12f);
+        for (int64_t j = 0; j < D; ++j) yi[j] = xi[j] * inv * gamma[j] * scale;
+    }
+}
+
+/* model_bs_roformer.cu:205-230 (identical in model_mel_band_roformer.cu:487-513). */
+void orc_rope_table(int n, int dh, float* cos_out, float* sin_out) {
+    int half = dh / 2;
+    for (int p = 0; p < n; ++p)
+        for (int i = 0; i < half; ++i) {
+            float freq = 1.0f / powf(10000.0f, (float)(2 * i) / (float)dh);
+            float angle = (float)p * freq;
+            cos_out[p * half + i] = cosf(angle);
+            sin_out[p * half + i] = sinf(angle);
+        }
+}
+
+/* ops_misc.cu:39-69: pairs (2i, 2i+1) rotate by the angle of (n, i). */
+void orc_rope_apply(float* q, float* k, const float* cos_t, const float* sin_t,
+                    int64_t B, int64_t H, int64_t N, int64_t D) {
+    int64_t half = D / 2;
+#pragma omp parallel for schedule(static)
+    for (int64_t row = 0; row < B * H * N; ++row) {
+        int64_t n = row % N;
+        float* qr = q + row * D;
+        float* kr = k + row * D;
+        for (int64_t i = 0; i < half; ++i) {
+            float c = cos_t[n * half + i], s = sin_t[n * half + i];
+            float q0 = qr[2 * i], q1 = qr[2 * i + 1];
+            qr[2 * i] = q0 * c - q1 * s;
+            qr[2 * i + 1] = q0 * s + q1 * c;
+            float k0 = kr[2 * i], k1 = kr[2 * i + 1];
+            kr[2 * i] = k0 * c - k1 * s;
+            kr[2 * i + 1] = k0 * s + k1 * c;
+        }
+    }
+}
+
+/* ops_attention.cu:96-181 (S = Q.K^T, softmax rows, O = P.V) and the
+ * fused softmax of :390-452 (scale, row max, exp, sum, normalise). */
+void orc_attention(const float* q, const float* k, const float* v, float* out,
+                   int64_t B, int64_t H, int64_t N, int64_t Nk, int64_t D,
+                   float scale) {
+    int64_t BH = B * H;
+#pragma omp parallel
+    {
+        float* srow = (float*)malloc((size_t)(Nk > 0 ? Nk : 1) * sizeof(float));
+        float* acc = (float*)malloc((size_t)(D > 0 ? D : 1) * sizeof(float));
+#pragma omp for schedule(dynamic, 1) collapse(2)
+        for (int64_t bh = 0; bh < BH; ++bh) {
+            for (int64_t i = 0; i < N; ++i) {
+                const float* qi = q + (bh * N + i) * D;
+                const float* kb = k + bh * Nk * D;
+                const float* vb = v + bh * Nk * D;
+                float mx = -INFINITY;
+                int64_t D8 = D & ~(int64_t)7;
+                for (int64_t j = 0; j < Nk; ++j) {
+                    const float* kj = kb + j * D;
+                    v8f s8 = {0, 0, 0, 0, 0, 0, 0, 0};
+                    for (int64_t d = 0; d < D8; d += 8)
+                        s8 += *(const v8f*)(qi + d) * *(const v8f*)(kj + d);
+                    float s = ((s8[0] + s8[1]) + (s8[2] + s8[3])) +
+                              ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+                    for (int64_t d = D8; d < D; ++d) s += qi[d] * kj[d];
+                    s *= scale;
+                    srow[j] = s;
+                    if (s > mx) mx = s;
+                }
+                float sum = 0.0f;
+                for (int64_t j = 0; j < Nk; ++j) {
+                    float e = expf(srow[j] - mx);
+                    srow[j] = e;
+                    sum += e;
+                }
+                float inv = 1.0f / sum;
+                for (int64_t d = 0; d < D; ++d) acc[d] = 0.0f;
+                for (int64_t j = 0; j < Nk; ++j) {
+                    float p = srow[j] * inv;
+                    const float* vj = vb + j * D;
+                    for (int64_t d = 0; d < D; ++d) acc[d] += p * vj[d];
+                }
+                float* oi = out + (bh * N + i) * D;
+                for (int64_t d = 0; d < D; ++d) oi[d] = acc[d];
+            }
+        }
+        free(srow);
+        free(acc);
+    }
+}
+
+/* model_mel_band_roformer.cu:34-52: qkv row layout is (qkv, h, d). */
+void orc_split_qkv(const float* qkv, float* q, float* k, float* v,
+                   int64_t B, int64_t N, int64_t H, int64_t D) {
+    int64_t HD = H * D;
+#pragma omp parallel for schedule(static) collapse(2)
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t n = 0; n < N; ++n) {
+            const float* row = qkv + (b * N + n) * 3 * HD;
+            for (int64_t h = 0; h < H; ++h) {
+                int64_t o = ((b * H + h) * N + n) * D;
+                memcpy(q + o, row + h * D, (size_t)D * sizeof(float));
+                memcpy(k + o, row + HD + h * D, (size_t)D * sizeof(float));
+                memcpy(v + o, row + 2 * HD + h * D, (size_t)D * sizeof(float));
+            }
+        }
+}
+
+/* model_mel_band_roformer.cu:76-93 (BSR: model_bs_roformer.cu:266-278). */
+void orc_gate_merge(const float* o, const float* gates, float* merged,
+                    int64_t B, int64_t H, int64_t N, int64_t D) {
+#pragma omp parallel for schedule(static) collapse(2)
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t n = 0; n < N; ++n)
+            for (int64_t h = 0; h < H; ++h) {
+                float g = gates[(b * N + n) * H + h];
+                const float* src = o + ((b * H + h) * N + n) * D;
+                float* dst = merged + (b * N + n) * H * D + h * D;
+                for (int64_t d = 0; d < D; ++d) dst[d] = src[d] * g;
+            }
+}
+
+static float* xalloc(int64_t n) {
+    float* p = (float*)malloc((size_t)(n > 0 ? n : 1) * sizeof(float));
+    if (!p) abort();
+    return p;
+}
+
+/* model_bs_roformer.cu:236-331 / model_mel_band_roformer.cu:519-651. */
+void orc_transformer(float* x, int64_t B, int64_t N, int64_t dim, int64_t H,
+                     int64_t Dh, int64_t ff, const orc_layer_weights* w,
+                     const float* cos_t, const float* sin_t) {
+    int64_t M = B * N, HD = H * Dh;
+    float scale = sqrtf((float)dim);
+    float* normed = xalloc(M * dim);
+    float* qkv = xalloc(M * 3 * HD);
+    float* q = xalloc(M * HD);
+    float* k = xalloc(M * HD);
+    float* v = xalloc(M * HD);
+    float* o = xalloc(M * HD);
+    float* gates = xalloc(M * H);
+    float* merged = xalloc(M * HD);
+    float* hbuf = xalloc(M * ff);
+
+    /* Attention block: model_bs_roformer.cu:242-283. */
+    orc_rms_norm(x, w->attn_gamma, scale, normed, M, dim);
+    orc_linear(normed, w->w_qkv, NULL, NULL, qkv, M, dim, 3 * HD, ORC_ACT_NONE);
+    orc_split_qkv(qkv, q, k, v, B, N, H, Dh);
+    orc_rope_apply(q, k, cos_t, sin_t, B, H, N, Dh);
+    orc_attention(q, k, v, o, B, H, N, N, Dh, 1.0f / sqrtf((float)Dh));
+    orc_linear(normed, w->w_gate, w->b_gate, NULL, gates, M, dim, H, ORC_ACT_SIGMOID);
+    orc_gate_merge(o, gates, merged, B, H, N, Dh);
+    /* x = x + to_out(merged)   (model_bs_roformer.cu:321-322) */
+    orc_linear(merged, w->w_out, NULL, x, x, M, HD, dim, ORC_ACT_NONE);
+
+    /* Feed-forward block: model_bs_roformer.cu:290-304, :325-326. */
+    orc_rms_norm(x, w->ff_gamma, scale, normed, M, dim);
+    orc_linear(normed, w->w_ff1, w->b_ff1, NULL, hbuf, M, dim, ff, ORC_ACT_GELU);
+    orc_linear(hbuf, w->w_ff2, w->b_ff2, x, x, M, ff, dim, ORC_ACT_NONE);
+
+    /* MelBandRoformer per-transformer output norm (:647-648). */
+    if (w->final_gamma) {
+        orc_rms_norm(x, w->final_gamma, scale, normed, M, dim);
+        memcpy(x, normed, (size_t)(M * dim) * sizeof(float));
+    }
+    free(normed); free(qkv); free(q); free(k); free(v); free(o);
+    free(gates); free(merged); free(hbuf);
+}
+
+/* [A,B',C',D'] <-> [A,C',B',D'] permute of the middle two axes. */
+static void swap12(const float* src, float* dst, int64_t A, int64_t P, int64_t Q,
+                   int64_t D) {
+#pragma omp parallel for schedule(static) collapse(2)
+    for (int64_t a = 0; a < A; ++a)
+        for (int64_t p = 0; p < P; ++p)
+            for (int64_t qq = 0; qq < Q; ++qq)
+                memcpy(dst + ((a * Q + qq) * P + p) * D,
+                       src + ((a * P + p) * Q + qq) * D, (size_t)D * sizeof(float));
+}
+
+/* model_bs_roformer.cu:482-539 / model_mel_band_roformer.cu:843-906. */
+void orc_roformer_stack(float* x, int64_t B, int64_t T, int64_t F, int64_t dim,
+                        int64_t H, int64_t Dh, int64_t ff, int64_t depth,
+                        const orc_layer_weights* layers,
+                        const float* final_gamma) {
+    int64_t half = Dh / 2;
+    float* tcos = xalloc(T * half);
+    float* tsin = xalloc(T * half);
+    float* fcos = xalloc(F * half);
+    float* fsin = xalloc(F * half);
+    orc_rope_table((int)T, (int)Dh, tcos, tsin);
+    orc_rope_table((int)F, (int)Dh, fcos, fsin);
+    float* tmp = xalloc(B * T * F * dim);
+    for (int64_t d = 0; d < depth; ++d) {
+        /* [B,T,F,dim] -> [B,F,T,dim]; time transformer on [B*F, T, dim]. */
+        swap12(x, tmp, B, T, F, dim);
+        orc_transformer(tmp, B * F, T, dim, H, Dh, ff, &layers[2 * d], tcos, tsin);
+        /* back to [B,T,F,dim]; frequency transformer on [B*T, F, dim]. */
+        swap12(tmp, x, B, F, T, dim);
+        orc_transformer(x, B * T, F, dim, H, Dh, ff, &layers[2 * d + 1], fcos, fsin);
+    }
+    if (final_gamma) {
+        orc_rms_norm(x, final_gamma, sqrtf((float)dim), tmp, B * T * F, dim);
+        memcpy(x, tmp, (size_t)(B * T * F * dim) * sizeof(float));
+    }
+    free(tmp); free(tcos); free(tsin); free(fcos); free(fsin);
+}

@@ -1,0 +1,207 @@
+"""ctypes wrapper of the CPU oracle (oracle/_build/libmsst_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: the parity checker for the HIP path and the timed
+CPU baseline of bench.py.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg import this module; the product never does.
+
+All arrays are numpy float32, C-contiguous.  Functions return new arrays and
+never modify their inputs, except where the name says `_inplace`.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from dataclasses import dataclass, fields
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libmsst_oracle.so")
+
+ACT = {"none": 0, "gelu": 1, "sigmoid": 2, "silu": 3}
+
+_lib = None
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (gcc, OpenMP)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_fp = ctypes.POINTER(ctypes.c_float)
+_i64 = ctypes.c_int64
+
+
+class LayerWeightsC(ctypes.Structure):
+    _fields_ = [(n, _fp) for n in (
+        "attn_gamma", "w_qkv", "w_gate", "b_gate", "w_out", "ff_gamma",
+        "w_ff1", "b_ff1", "w_ff2", "b_ff2", "final_gamma")]
+
+
+def _declare(l: ctypes.CDLL) -> None:
+    l.orc_num_threads.restype = ctypes.c_int
+    l.orc_set_num_threads.argtypes = [ctypes.c_int]
+    l.orc_linear.argtypes = [_fp, _fp, _fp, _fp, _fp, _i64, _i64, _i64, ctypes.c_int]
+    l.orc_activation.argtypes = [_fp, _fp, _i64, ctypes.c_int]
+    l.orc_rms_norm.argtypes = [_fp, _fp, ctypes.c_float, _fp, _i64, _i64]
+    l.orc_rope_table.argtypes = [ctypes.c_int, ctypes.c_int, _fp, _fp]
+    l.orc_rope_apply.argtypes = [_fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64]
+    l.orc_attention.argtypes = [_fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64, _i64,
+                                ctypes.c_float]
+    l.orc_split_qkv.argtypes = [_fp, _fp, _fp, _fp, _i64, _i64, _i64, _i64]
+    l.orc_gate_merge.argtypes = [_fp, _fp, _fp, _i64, _i64, _i64, _i64]
+    l.orc_transformer.argtypes = [_fp, _i64, _i64, _i64, _i64, _i64, _i64,
+                                  ctypes.POINTER(LayerWeightsC), _fp, _fp]
+    l.orc_roformer_stack.argtypes = [_fp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                     _i64, ctypes.POINTER(LayerWeightsC), _fp]
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a):
+    if a is None:
+        return None
+    return a.ctypes.data_as(_fp)
+
+
+def num_threads() -> int:
+    return lib().orc_num_threads()
+
+
+def set_num_threads(n: int) -> None:
+    lib().orc_set_num_threads(n)
+
+
+def linear(x, w, b=None, act="none", residual=None) -> np.ndarray:
+    x, w = _f32(x), _f32(w)
+    K = x.shape[-1]
+    N, Kw = w.shape
+    assert Kw == K
+    M = x.size // K
+    b = None if b is None else _f32(b)
+    r = None if residual is None else _f32(residual).reshape(M, N)
+    out = np.empty(x.shape[:-1] + (N,), np.float32)
+    lib().orc_linear(_p(x), _p(w), _p(b), _p(r), _p(out), M, K, N, ACT[act])
+    return out
+
+
+def activation(x, act) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().orc_activation(_p(x), _p(out), x.size, ACT[act])
+    return out
+
+
+def rms_norm(x, gamma, scale) -> np.ndarray:
+    x, g = _f32(x), _f32(gamma)
+    D = x.shape[-1]
+    out = np.empty_like(x)
+    lib().orc_rms_norm(_p(x), _p(g), float(scale), _p(out), x.size // D, D)
+    return out
+
+
+def rope_table(n: int, dh: int):
+    c = np.empty((n, dh // 2), np.float32)
+    s = np.empty((n, dh // 2), np.float32)
+    lib().orc_rope_table(n, dh, _p(c), _p(s))
+    return c, s
+
+
+def rope_apply(q, k, cos_t, sin_t):
+    q = _f32(q).copy()
+    k = _f32(k).copy()
+    B, H, N, D = q.shape
+    lib().orc_rope_apply(_p(q), _p(k), _p(_f32(cos_t)), _p(_f32(sin_t)), B, H, N, D)
+    return q, k
+
+
+def attention(q, k, v, scale=None) -> np.ndarray:
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    B, H, N, D = q.shape
+    Nk = k.shape[2]
+    if scale is None or scale == 0.0:
+        scale = 1.0 / np.sqrt(np.float32(D))
+    out = np.empty_like(q)
+    lib().orc_attention(_p(q), _p(k), _p(v), _p(out), B, H, N, Nk, D, float(scale))
+    return out
+
+
+def split_qkv(qkv, H, D):
+    qkv = _f32(qkv)
+    B, N, _ = qkv.shape
+    q = np.empty((B, H, N, D), np.float32)
+    k = np.empty_like(q)
+    v = np.empty_like(q)
+    lib().orc_split_qkv(_p(qkv), _p(q), _p(k), _p(v), B, N, H, D)
+    return q, k, v
+
+
+def gate_merge(o, gates) -> np.ndarray:
+    o, g = _f32(o), _f32(gates)
+    B, H, N, D = o.shape
+    out = np.empty((B, N, H * D), np.float32)
+    lib().orc_gate_merge(_p(o), _p(g), _p(out), B, H, N, D)
+    return out
+
+
+@dataclass
+class LayerWeights:
+    """fp32 weights of one transformer, nn.Linear layout ([out, in])."""
+    attn_gamma: np.ndarray
+    w_qkv: np.ndarray
+    w_gate: np.ndarray
+    b_gate: np.ndarray
+    w_out: np.ndarray
+    ff_gamma: np.ndarray
+    w_ff1: np.ndarray
+    b_ff1: np.ndarray
+    w_ff2: np.ndarray
+    b_ff2: np.ndarray
+    final_gamma: np.ndarray | None = None
+
+    def to_c(self) -> LayerWeightsC:
+        kw = {}
+        for f in fields(self):
+            a = getattr(self, f.name)
+            if a is not None:
+                a = _f32(a)
+                setattr(self, f.name, a)  # keep the contiguous copy alive
+            kw[f.name] = _p(a)
+        return LayerWeightsC(**kw)
+
+
+def transformer(x, w: LayerWeights, cos_t, sin_t, heads: int, dim_head: int) -> np.ndarray:
+    x = _f32(x).copy()
+    B, N, dim = x.shape
+    ff = w.w_ff1.shape[0]
+    wc = w.to_c()
+    cos_t, sin_t = _f32(cos_t), _f32(sin_t)
+    lib().orc_transformer(_p(x), B, N, dim, heads, dim_head, ff, ctypes.byref(wc),
+                          _p(cos_t), _p(sin_t))
+    return x
+
+
+def roformer_stack(x, layers, heads: int, dim_head: int, final_gamma=None) -> np.ndarray:
+    """x: [B, T, F, dim]; layers: [time0, freq0, time1, freq1, ...]."""
+    x = _f32(x).copy()
+    B, T, F, dim = x.shape
+    assert len(layers) % 2 == 0
+    ff = layers[0].w_ff1.shape[0]
+    arr = (LayerWeightsC * len(layers))(*[lw.to_c() for lw in layers])
+    fg = None if final_gamma is None else _f32(final_gamma)
+    lib().orc_roformer_stack(_p(x), B, T, F, dim, heads, dim_head, ff, len(layers) // 2,
+                             arr, _p(fg))
+    return x

@@ -1,0 +1,257 @@
+"""Kernel-level parity of the HIP path (through the C ABI) against the CPU
+oracle on identical seeded inputs.
+
+Tolerances (normwise max|y - r| / max|r|): 1e-4 for the fp32 path, 2e-2
+for the fp16 path (fp16 operands/outputs, fp32 accumulation).  For fp16 the
+oracle is fed the fp16-rounded operands, so the measured error is the
+kernel's own (accumulation order + output rounding).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import TOL_F16, TOL_F32, rel_err
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+def r16(a):
+    return a.astype(np.float16).astype(np.float32)
+
+
+def tdt(name):
+    return torch.float32 if name == "f32" else torch.float16
+
+
+def tol(name):
+    return TOL_F32 if name == "f32" else TOL_F16
+
+
+# ------------------------------------------------------------------ RMSNorm
+@pytest.mark.parametrize("rows,D", [(1, 4), (5, 7), (33, 384), (100, 512), (7, 1100),
+                                    (49662, 512), (48060, 384)])
+@pytest.mark.parametrize("xd,od", [("f32", "f32"), ("f32", "f16"), ("f16", "f16"), ("f16", "f32")])
+def test_rms_norm(msst, oracle, cuda, rows, D, xd, od):
+    rng = np.random.default_rng(rows * 7 + D)
+    x = rng.standard_normal((rows, D)).astype(np.float32)
+    if xd == "f16":
+        x = r16(x)
+    g = (1 + rng.standard_normal(D) * 0.02).astype(np.float32)
+    y = msst.rms_norm(dev(x, tdt(xd)), dev(g), math.sqrt(D), out_dtype=tdt(od))
+    r = oracle.rms_norm(x, g, math.sqrt(D))
+    assert rel_err(host(y), r) < (TOL_F32 if od == "f32" else 2e-3)
+
+
+@pytest.mark.parametrize("rows,D,G", [(3, 64, 8), (1000, 384, 8), (49662, 512, 8), (17, 100, 5),
+                                      (64, 512, 16), (9, 256, 12)])
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_rms_norm_gate(msst, oracle, cuda, rows, D, G, dt):
+    rng = np.random.default_rng(rows + D + G)
+    x = rng.standard_normal((rows, D)).astype(np.float32)
+    g = (1 + rng.standard_normal(D) * 0.02).astype(np.float32)
+    wg = (rng.standard_normal((G, D)) * 0.02).astype(np.float32)
+    bg = (rng.standard_normal(G) * 0.02).astype(np.float32)
+    if dt == "f16":
+        wg = r16(wg)
+    y, gates = msst.rms_norm_gate(dev(x), dev(g), math.sqrt(D), dev(wg, tdt(dt)), dev(bg),
+                                  out_dtype=tdt(dt))
+    yn = oracle.rms_norm(x, g, math.sqrt(D))
+    assert rel_err(host(y), yn) < (TOL_F32 if dt == "f32" else 2e-3)
+    yin = yn if dt == "f32" else r16(yn)
+    rg = oracle.linear(yin, wg, bg, "sigmoid")
+    assert rel_err(host(gates), rg) < TOL_F32
+
+
+# ------------------------------------------------------------------ linear
+SMALL = [(1, 64, 32), (31, 64, 8), (100, 384, 1536), (257, 512, 512), (1000, 72, 100),
+         (300, 2048, 384), (65, 50, 40), (600, 512, 8), (40, 136, 264)]
+
+
+@pytest.mark.parametrize("M,K,N", SMALL)
+@pytest.mark.parametrize("wd,xd,od", [("f16", "f16", "f16"), ("f16", "f32", "f32"),
+                                      ("f32", "f32", "f32"), ("f32", "f16", "f32")])
+@pytest.mark.parametrize("act", ["none", "gelu", "sigmoid"])
+def test_linear_small(msst, oracle, cuda, M, K, N, wd, xd, od, act):
+    rng = np.random.default_rng(M * 1000 + K + N)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal(N) * 0.02).astype(np.float32)
+    if xd == "f16":
+        x = r16(x)
+    if wd == "f16":
+        w = r16(w)
+        x = r16(x)  # the fp16 path rounds x as it is staged
+    y = msst.linear(dev(x, tdt(xd)), dev(w, tdt(wd)), dev(b), act, out_dtype=tdt(od))
+    r = oracle.linear(x, w, b, act)
+    assert rel_err(host(y), r) < tol(wd if od == "f32" else "f16")
+
+
+@pytest.mark.parametrize("wd", ["f16", "f32"])
+def test_linear_residual_in_place(msst, oracle, cuda, wd):
+    rng = np.random.default_rng(5)
+    M, K, N = 777, 512, 384
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    b = (rng.standard_normal(N) * 0.02).astype(np.float32)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    if wd == "f16":
+        x, w = r16(x), r16(w)
+    xr = dev(res)
+    msst.linear(dev(x, tdt(wd)), dev(w, tdt(wd)), dev(b), "none", residual=xr, out=xr)
+    r = oracle.linear(x, w, b, "none", residual=res)
+    assert rel_err(host(xr), r) < tol(wd)
+
+
+SWEEP_KN = [(384, 1536), (1536, 384), (512, 1536), (512, 2048), (2048, 512), (384, 8), (512, 8),
+            (512, 384), (512, 512)]
+
+
+@pytest.mark.parametrize("M", [48060, 49662, 198648])
+@pytest.mark.parametrize("K,N", SWEEP_KN)
+@pytest.mark.parametrize("wd", ["f16", "f32"])
+def test_linear_baseline_sweep(msst, oracle, cuda, M, K, N, wd):
+    """The BASELINE GEMM sweep shapes, all three epilogues, checked on a
+    sample of rows (every output row depends only on its own input row, so
+    the sample check is exact parity on those rows)."""
+    g = torch.Generator(device="cuda").manual_seed(M + K * 7 + N)
+    x = torch.randn(M, K, device="cuda", generator=g)
+    w = torch.randn(N, K, device="cuda", generator=g) * 0.02
+    b = torch.randn(N, device="cuda", generator=g) * 0.02
+    if wd == "f16":
+        x, w = x.half(), w.half()
+    rows = torch.cat([torch.arange(0, 64), torch.arange(M - 64, M),
+                      torch.randint(0, M, (512,), generator=torch.Generator().manual_seed(M))])
+    xs = x[rows.cuda()].float().cpu().numpy()
+    ws, bs = w.float().cpu().numpy(), b.cpu().numpy()
+    for act in ("none", "gelu", "sigmoid"):
+        od = torch.float16 if wd == "f16" else torch.float32
+        y = msst.linear(x, w, b, act, out_dtype=od)
+        ys = y[rows.cuda()].float().cpu().numpy()
+        r = oracle.linear(xs, ws, bs, act)
+        e = rel_err(ys, r)
+        assert e < tol(wd), (act, e)
+        del y
+
+
+# -------------------------------------------------------------------- RoPE
+@pytest.mark.parametrize("B,H,N,D", [(1, 1, 1, 64), (2, 8, 62, 64), (3, 8, 801, 64), (1, 2, 5, 6)])
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_rope_qk(msst, oracle, cuda, B, H, N, D, dt):
+    rng = np.random.default_rng(N + D)
+    q = rng.standard_normal((B, H, N, D)).astype(np.float32)
+    k = rng.standard_normal((B, H, N, D)).astype(np.float32)
+    if dt == "f16":
+        q, k = r16(q), r16(k)
+    c, s = oracle.rope_table(N, D)
+    qd, kd = dev(q, tdt(dt)), dev(k, tdt(dt))
+    msst.rope_qk_(qd, kd, dev(c), dev(s))
+    qr, kr = oracle.rope_apply(q, k, c, s)
+    t = TOL_F32 if dt == "f32" else 2e-3
+    assert rel_err(host(qd), qr) < t
+    assert rel_err(host(kd), kr) < t
+
+
+def test_rope_table_device(msst, oracle, cuda):
+    """Same angles as the host table; cos/sin within a couple of ulps."""
+    for n in (1, 62, 801):
+        c, s = msst.rope_table_device(n, 64)
+        oc, os_ = oracle.rope_table(n, 64)
+        np.testing.assert_allclose(host(c), oc, rtol=0, atol=2.5e-7)
+        np.testing.assert_allclose(host(s), os_, rtol=0, atol=2.5e-7)
+
+
+# --------------------------------------------------------------- attention
+ATTN = [(1, 1, 1, 1), (2, 3, 17, 19), (1, 2, 62, 62), (2, 8, 60, 60), (1, 3, 64, 64),
+        (1, 2, 65, 65), (1, 2, 129, 70), (2, 8, 801, 801), (1, 1, 300, 1000)]
+
+
+@pytest.mark.parametrize("B,H,N,Nk", ATTN)
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_attention(msst, oracle, cuda, B, H, N, Nk, dt):
+    rng = np.random.default_rng(N * 31 + Nk)
+    q = rng.standard_normal((B, H, N, 64)).astype(np.float32)
+    k = rng.standard_normal((B, H, Nk, 64)).astype(np.float32)
+    v = rng.standard_normal((B, H, Nk, 64)).astype(np.float32)
+    if dt == "f16":
+        q, k, v = r16(q), r16(k), r16(v)
+    y = msst.attention(dev(q, tdt(dt)), dev(k, tdt(dt)), dev(v, tdt(dt)))
+    r = oracle.attention(q, k, v)
+    assert rel_err(host(y), r) < tol(dt)
+
+
+def _fused_reference(oracle, qkv, gates, cos_t, sin_t, B, F, T, H, axis):
+    """Oracle path for one attention block on [B,F,T] token order."""
+    D = 64
+    if axis == "time":
+        seqs = qkv.reshape(B * F, T, 3 * H * D)
+        g = gates.reshape(B * F, T, H)
+    else:
+        seqs = qkv.reshape(B, F, T, 3 * H * D).transpose(0, 2, 1, 3).reshape(B * T, F, 3 * H * D)
+        g = gates.reshape(B, F, T, H).transpose(0, 2, 1, 3).reshape(B * T, F, H)
+    q, k, v = oracle.split_qkv(seqs, H, D)
+    if cos_t is not None:
+        q, k = oracle.rope_apply(q, k, cos_t, sin_t)
+    o = oracle.attention(q, k, v)
+    m = oracle.gate_merge(o, g)
+    if axis == "time":
+        return m.reshape(B * F * T, H * D)
+    return m.reshape(B, T, F, H * D).transpose(0, 2, 1, 3).reshape(B * F * T, H * D)
+
+
+@pytest.mark.parametrize("B,F,T", [(1, 3, 70), (2, 5, 33), (1, 62, 801), (1, 60, 801)])
+@pytest.mark.parametrize("axis", ["time", "freq"])
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_gated_rope_attention(msst, oracle, cuda, B, F, T, axis, dt):
+    H, D = 8, 64
+    rng = np.random.default_rng(B * 100 + F * 10 + T)
+    M = B * F * T
+    qkv = rng.standard_normal((M, 3 * H * D)).astype(np.float32)
+    if dt == "f16":
+        qkv = r16(qkv)
+    gates = rng.uniform(0.0, 1.0, (M, H)).astype(np.float32)
+    n = T if axis == "time" else F
+    c, s = oracle.rope_table(n, D)
+    if axis == "time":
+        L = msst.seq_layout(B * F, 1, T, T, 0, 1)
+    else:
+        L = msst.seq_layout(B, T, F, F * T, 1, T)
+    y = msst.gated_rope_attention(dev(qkv, tdt(dt)), L, H, dev(c), dev(s), dev(gates))
+    r = _fused_reference(oracle, qkv, gates, c, s, B, F, T, H, axis)
+    assert rel_err(host(y), r) < tol(dt)
+
+
+# ----------------------------------------------------------------- layout
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_layout_kernels(msst, cuda, dt):
+    B, N, H, D = 2, 7, 3, 64
+    qkv = np.arange(B * N * 3 * H * D, dtype=np.float32).reshape(B, N, 3 * H * D) % 1000
+    q, k, v = msst.split_qkv_heads(dev(qkv, tdt(dt)), H)
+    ref = qkv.reshape(B, N, 3, H, D).transpose(2, 0, 3, 1, 4)
+    np.testing.assert_array_equal(host(q), ref[0])
+    np.testing.assert_array_equal(host(k), ref[1])
+    np.testing.assert_array_equal(host(v), ref[2])
+    gates = np.full((B, N, H), 0.5, np.float32)
+    m = msst.gate_merge_heads(q, dev(gates))
+    np.testing.assert_array_equal(host(m), (ref[0] * 0.5).transpose(0, 2, 1, 3).reshape(B, N, H * D))
+    x = np.random.default_rng(0).standard_normal((3, 5, 4, 12)).astype(np.float32)
+    sw = msst.swap_axes12(dev(x, tdt(dt)))
+    np.testing.assert_array_equal(host(sw), r16(x).transpose(0, 2, 1, 3) if dt == "f16"
+                                  else x.transpose(0, 2, 1, 3))
+    a, b = dev(x), dev(2 * x)
+    np.testing.assert_allclose(host(msst.add(a, b)), 3 * x, rtol=1e-6)
+    np.testing.assert_array_equal(host(msst.cast(a, torch.float16)), r16(x))

@@ -1,0 +1,128 @@
+"""Layer- and stack-level parity of the HIP Roformer path against the CPU
+oracle, at the BASELINE configurations.
+
+  config 1  MelBandRoformer time layer, fp32, x [60, 801, 384]      (full size)
+  config 3  MelBandRoformer stack, fp16, dim 384, [60 bands, 801]   (depth 1 at
+            full size vs the oracle; depth 6 through the property tests)
+  config 4  BSRoformer stack, fp16, dim 512, [62 bands, 801]        (same)
+  config 5  BSRoformer, batch of 4 chunks                           (batch
+            consistency: bit-identical to 4 single-chunk runs)
+Weights: matrices and biases ~ N(0, 0.02), gammas 1 + N(0, 0.02), x ~ N(0,1).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import torch_ref as R
+from conftest import TOL_F16, TOL_F32, rel_err
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+MATS = ("w_qkv", "w_gate", "w_out", "w_ff1", "w_ff2")
+
+
+def make_layers(seed, n, dim, heads, ff, fp16, final_norm):
+    rng = np.random.default_rng(seed)
+    layers = [R.random_layer(rng, dim, heads, 64, ff, final_norm=final_norm) for _ in range(n)]
+    if fp16:
+        for w in layers:
+            for m in MATS:
+                w[m] = w[m].astype(np.float16).astype(np.float32)
+    return layers
+
+
+def upload(layers, fp16):
+    out = []
+    for w in layers:
+        d = {}
+        for k, v in w.items():
+            if v is None:
+                continue
+            t = torch.from_numpy(np.ascontiguousarray(v)).cuda()
+            if fp16 and k in MATS:
+                t = t.half()
+            d[k] = t
+        out.append(d)
+    return out
+
+
+def build_stack(msst, layers, fp16, B, T, F, dim, heads, ff, final_gamma=None):
+    dl = upload(layers, fp16)
+    fg = None if final_gamma is None else torch.from_numpy(final_gamma).cuda()
+    st = msst.RoformerStack(dl, fg, B, T, F, dim, heads, 64, ff, msst.F16 if fp16 else msst.F32)
+    st._keep = dl
+    return st
+
+
+def run_stack(msst, oracle, B, T, F, dim, heads, ff, depth, fp16, mbr, seed=0):
+    layers = make_layers(seed, 2 * depth, dim, heads, ff, fp16, final_norm=mbr)
+    rng = np.random.default_rng(seed + 99)
+    fg = None if mbr else (1 + rng.standard_normal(dim) * 0.02).astype(np.float32)
+    x = rng.standard_normal((B, T, F, dim)).astype(np.float32)
+    st = build_stack(msst, layers, fp16, B, T, F, dim, heads, ff, fg)
+    xd = torch.from_numpy(x).cuda()
+    st(xd)
+    torch.cuda.synchronize()
+    y = xd.cpu().numpy()
+    r = oracle.roformer_stack(x, [oracle.LayerWeights(**w) for w in layers], heads, 64, fg)
+    return rel_err(y, r)
+
+
+@pytest.mark.parametrize("fp16", [False, True])
+@pytest.mark.parametrize("mbr", [False, True])
+@pytest.mark.parametrize("B,T,F,dim,heads,ff,depth", [(1, 70, 5, 128, 2, 512, 2),
+                                                      (2, 33, 7, 192, 3, 256, 1),
+                                                      (1, 130, 62, 128, 2, 256, 1)])
+def test_stack_small(msst, oracle, cuda, B, T, F, dim, heads, ff, depth, fp16, mbr):
+    e = run_stack(msst, oracle, B, T, F, dim, heads, ff, depth, fp16, mbr)
+    assert e < (TOL_F16 if fp16 else TOL_F32), e
+
+
+def test_config1_mbr_time_layer_fp32(msst, oracle, cuda):
+    """Single MelBandRoformer time layer, fp32, x [60, 801, 384], N(0,1)."""
+    F, T, dim, heads, ff = 60, 801, 384, 8, 1536
+    layers = make_layers(0, 2, dim, heads, ff, False, final_norm=False)
+    x = np.random.default_rng(0).standard_normal((F, T, dim)).astype(np.float32)
+    st = build_stack(msst, layers, False, 1, T, F, dim, heads, ff)
+    xd = torch.from_numpy(x).cuda()
+    st.transformer(xd, 0, 0)
+    torch.cuda.synchronize()
+    c, s = oracle.rope_table(T, 64)
+    r = oracle.transformer(x, oracle.LayerWeights(**layers[0]), c, s, heads, 64)
+    e = rel_err(xd.cpu().numpy(), r)
+    assert e < TOL_F32, e
+
+
+@pytest.mark.parametrize("name,F,dim,ff,mbr", [("bsr", 62, 512, 2048, False),
+                                               ("mbr", 60, 384, 1536, True)])
+def test_full_size_depth1_fp16(msst, oracle, cuda, name, F, dim, ff, mbr):
+    """Configs 3/4 at full spatial size, one depth (time + freq layer)."""
+    e = run_stack(msst, oracle, 1, 801, F, dim, 8, ff, 1, True, mbr, seed=4)
+    assert e < TOL_F16, e
+
+
+@pytest.mark.parametrize("name,F,dim,ff,depth,mbr", [("bsr", 62, 512, 2048, 12, False),
+                                                     ("mbr", 60, 384, 1536, 6, True)])
+def test_full_depth_properties(msst, cuda, name, F, dim, ff, depth, mbr):
+    """Configs 3/4 at full depth: finite, deterministic, and the batch-of-4
+    run (config 5 for BSR) equals four single-chunk runs bit for bit — every
+    kernel's per-row / per-sequence arithmetic is independent of the batch."""
+    T, heads = 801, 8
+    layers = make_layers(5, 2 * depth, dim, heads, ff, True, final_norm=mbr)
+    rng = np.random.default_rng(6)
+    fg = None if mbr else (1 + rng.standard_normal(dim) * 0.02).astype(np.float32)
+    x = torch.from_numpy(rng.standard_normal((4, T, F, dim)).astype(np.float32)).cuda()
+    st4 = build_stack(msst, layers, True, 4, T, F, dim, heads, ff, fg)
+    st1 = build_stack(msst, layers, True, 1, T, F, dim, heads, ff, fg)
+    y4 = st4(x.clone())
+    singles = [st1(x[i:i + 1].clone()) for i in range(4)]
+    again = st1(x[0:1].clone())
+    torch.cuda.synchronize()
+    assert torch.isfinite(y4).all()
+    for i in range(4):
+        assert torch.equal(y4[i:i + 1], singles[i]), i
+    assert torch.equal(again, singles[0])
+    # the stack changed the input substantially (it is not an identity)
+    assert (y4 - x).abs().max().item() > 0.1

@@ -1,0 +1,212 @@
+"""Pins the C oracle (oracle/msst_oracle.c) before it is trusted as the
+parity checker of the HIP path.
+
+Each oracle function is checked against something it does not share code
+with: numpy/torch library routines in float64, closed forms, invariants of
+the mathematics and brute force on tiny inputs — chosen so a dropped term,
+a wrong sign or index, or a transposed operand fails at least one check.
+The reference itself (CUDA + cuBLAS) cannot be built or run here and holds
+no golden vectors, so these are the pins.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import torch_ref as R
+from conftest import rel_err
+
+RNG = np.random.default_rng(1234)
+
+
+def rnd(*shape, s=1.0):
+    return (RNG.standard_normal(shape) * s).astype(np.float32)
+
+
+# --------------------------------------------------------------------- linear
+@pytest.mark.parametrize("M,K,N", [(1, 1, 1), (7, 5, 3), (13, 96, 50), (37, 130, 17),
+                                   (64, 384, 96)])
+@pytest.mark.parametrize("act", ["none", "gelu", "sigmoid", "silu"])
+def test_linear_matches_float64_library(oracle, M, K, N, act):
+    x, w, b = rnd(M, K), rnd(N, K, s=0.02), rnd(N, s=0.02)
+    y = oracle.linear(x, w, b, act)
+    r = R.linear(x, w, b, act).numpy()
+    assert rel_err(y, r) < 1e-6
+
+
+def test_linear_residual_and_no_bias(oracle):
+    x, w, res = rnd(9, 40), rnd(11, 40), rnd(9, 11)
+    y = oracle.linear(x, w, None, "none", residual=res)
+    r = x.astype(np.float64) @ w.T.astype(np.float64) + res
+    assert rel_err(y, r) < 1e-6
+
+
+def test_linear_identity_and_selection(oracle):
+    x = rnd(10, 16)
+    np.testing.assert_array_equal(oracle.linear(x, np.eye(16, dtype=np.float32)), x)
+    perm = RNG.permutation(16)[:5]
+    sel = np.eye(16, dtype=np.float32)[perm]          # W rows are one-hot
+    np.testing.assert_array_equal(oracle.linear(x, sel), x[:, perm])
+    b = rnd(5)
+    y = oracle.linear(np.zeros((3, 16), np.float32), sel, b)
+    np.testing.assert_array_equal(y, np.broadcast_to(b, (3, 5)))
+
+
+# ---------------------------------------------------------------- activations
+def test_activation_closed_forms(oracle):
+    z = np.zeros(4, np.float32)
+    assert np.all(oracle.activation(z, "gelu") == 0.0)
+    assert np.all(oracle.activation(z, "sigmoid") == 0.5)
+    x = np.linspace(-8, 8, 101).astype(np.float32)
+    s = oracle.activation(x, "sigmoid")
+    np.testing.assert_allclose(s + oracle.activation(-x, "sigmoid"), 1.0, atol=1e-6)
+    big = np.array([10.0, 20.0], np.float32)
+    np.testing.assert_allclose(oracle.activation(big, "gelu"), big, rtol=1e-6)
+    np.testing.assert_allclose(oracle.activation(-big, "gelu"), 0.0, atol=1e-6)
+    np.testing.assert_allclose(oracle.activation(x, "silu"), x * s, rtol=2e-6, atol=1e-7)
+
+
+# ------------------------------------------------------------------- rms_norm
+@pytest.mark.parametrize("rows,D", [(1, 1), (5, 7), (33, 384), (8, 512), (3, 1100)])
+def test_rms_norm_matches_normalize(oracle, rows, D):
+    x, g = rnd(rows, D), (1 + rnd(D, s=0.02))
+    y = oracle.rms_norm(x, g, math.sqrt(D))
+    r = R.rms_norm(x, g, math.sqrt(D)).numpy()
+    assert rel_err(y, r) < 1e-6
+
+
+def test_rms_norm_closed_forms(oracle):
+    D = 64
+    g = np.ones(D, np.float32)
+    for c in (0.5, -3.0, 100.0):
+        y = oracle.rms_norm(np.full((1, D), c, np.float32), g, math.sqrt(D))
+        np.testing.assert_allclose(y, np.sign(c), rtol=1e-6)
+    x = rnd(4, D)
+    np.testing.assert_allclose(oracle.rms_norm(7.5 * x, g, 2.0), oracle.rms_norm(x, g, 2.0),
+                               rtol=2e-6, atol=1e-7)
+    y = oracle.rms_norm(x, g, math.sqrt(D))
+    np.testing.assert_allclose(np.sum(y.astype(np.float64) ** 2, -1), D, rtol=1e-5)
+    # epsilon lives inside the sqrt: a zero row stays finite and zero
+    assert np.all(oracle.rms_norm(np.zeros((1, D), np.float32), g, 1.0) == 0.0)
+
+
+# ----------------------------------------------------------------------- RoPE
+@pytest.mark.parametrize("n,dh", [(1, 64), (62, 64), (801, 64), (9, 16)])
+def test_rope_table_geometry(oracle, n, dh):
+    c, s = oracle.rope_table(n, dh)
+    assert c.shape == (n, dh // 2)
+    np.testing.assert_allclose(c.astype(np.float64) ** 2 + s.astype(np.float64) ** 2, 1.0,
+                               atol=1e-6)
+    np.testing.assert_array_equal(c[0], 1.0)
+    np.testing.assert_array_equal(s[0], 0.0)
+    ang = R.rope_angles(n, dh).numpy()
+    # float32 angle n*freq carries ~n*ulp error; compare on the circle
+    err = np.abs(np.angle(np.exp(1j * ang) * (c - 1j * s)))
+    assert err.max() < 1e-6 * max(n, 1) + 1e-6
+    # i = 0 rotates by exactly one radian per position
+    np.testing.assert_allclose(c[:, 0], np.cos(np.arange(n, dtype=np.float32)), atol=1e-6)
+
+
+def test_rope_apply_matches_complex_rotation(oracle):
+    B, H, N, D = 2, 3, 11, 16
+    q, k = rnd(B, H, N, D), rnd(B, H, N, D)
+    c, s = oracle.rope_table(N, D)
+    qr, kr = oracle.rope_apply(q, k, c, s)
+    ang = torch.as_tensor(np.arctan2(s, c), dtype=torch.float64)
+    assert rel_err(qr, R.rope(q, ang).numpy()) < 1e-6
+    assert rel_err(kr, R.rope(k, ang).numpy()) < 1e-6
+    np.testing.assert_array_equal(qr[:, :, 0], q[:, :, 0])  # position 0 is identity
+    pair = lambda a: np.sqrt(a[..., 0::2] ** 2 + a[..., 1::2] ** 2)
+    np.testing.assert_allclose(pair(qr), pair(q), rtol=1e-5)
+
+
+def test_rope_relative_position(oracle):
+    """<R_m q, R_n k> depends only on m - n."""
+    D, N = 16, 20
+    base_q, base_k = rnd(D), rnd(D)
+    q = np.broadcast_to(base_q, (1, 1, N, D)).copy()
+    k = np.broadcast_to(base_k, (1, 1, N, D)).copy()
+    c, s = oracle.rope_table(N, D)
+    qr, kr = oracle.rope_apply(q, k, c, s)
+    dots = qr[0, 0] @ kr[0, 0].T
+    for off in (-3, 0, 5):
+        diag = np.diagonal(dots, offset=off)
+        np.testing.assert_allclose(diag, diag[0], rtol=1e-4, atol=1e-4)
+
+
+# ------------------------------------------------------------------ attention
+@pytest.mark.parametrize("B,H,N,Nk,D", [(1, 1, 1, 1, 8), (2, 3, 17, 19, 32), (1, 2, 62, 62, 64),
+                                        (1, 1, 129, 70, 64)])
+def test_attention_matches_sdpa(oracle, B, H, N, Nk, D):
+    q, k, v = rnd(B, H, N, D), rnd(B, H, Nk, D), rnd(B, H, Nk, D)
+    y = oracle.attention(q, k, v)
+    assert rel_err(y, R.attention(q, k, v).numpy()) < 1e-6
+
+
+def test_attention_closed_forms(oracle):
+    B, H, N, D = 1, 2, 9, 16
+    v = rnd(B, H, N, D)
+    q0 = np.zeros((B, H, N, D), np.float32)
+    y = oracle.attention(q0, rnd(B, H, N, D), v)
+    np.testing.assert_allclose(y, np.broadcast_to(v.mean(2, keepdims=True), y.shape), rtol=1e-5,
+                               atol=1e-6)
+    # one very peaked key per query selects that key's value row
+    k = np.eye(N, D, dtype=np.float32)[None, None].repeat(H, 1) * 50.0
+    qs = k.copy()
+    y = oracle.attention(qs, k, v, scale=1.0)
+    np.testing.assert_allclose(y, v, rtol=1e-5, atol=1e-5)
+
+
+# -------------------------------------------------------- head split / merge
+def test_split_and_merge_index_identities(oracle):
+    B, N, H, D = 2, 5, 3, 4
+    qkv = np.arange(B * N * 3 * H * D, dtype=np.float32).reshape(B, N, 3 * H * D)
+    q, k, v = oracle.split_qkv(qkv, H, D)
+    r = qkv.reshape(B, N, 3, H, D).transpose(2, 0, 3, 1, 4)
+    np.testing.assert_array_equal(q, r[0])
+    np.testing.assert_array_equal(k, r[1])
+    np.testing.assert_array_equal(v, r[2])
+    gates = (np.arange(B * N * H, dtype=np.float32).reshape(B, N, H) + 1) / 7
+    m = oracle.gate_merge(q, gates)
+    exp = (q * gates.transpose(0, 2, 1)[..., None]).transpose(0, 2, 1, 3).reshape(B, N, H * D)
+    np.testing.assert_array_equal(m, exp)
+
+
+# ---------------------------------------------------------- layer and stack
+@pytest.mark.parametrize("final", [False, True])
+def test_transformer_matches_torch_composition(oracle, final):
+    rng = np.random.default_rng(7)
+    B, N, dim, H, Dh, ff = 3, 13, 32, 2, 16, 64
+    w = R.random_layer(rng, dim, H, Dh, ff, final_norm=final)
+    x = rng.standard_normal((B, N, dim)).astype(np.float32)
+    c, s = oracle.rope_table(N, Dh)
+    y = oracle.transformer(x, oracle.LayerWeights(**w), c, s, H, Dh)
+    ang = torch.as_tensor(np.arctan2(s, c), dtype=torch.float64)
+    r = R.transformer(x, w, H, Dh, ang).numpy()
+    assert rel_err(y, r) < 2e-6
+
+
+def test_stack_matches_torch_composition(oracle):
+    rng = np.random.default_rng(11)
+    B, T, Fb, dim, H, Dh, ff, depth = 2, 9, 5, 32, 2, 16, 64, 2
+    layers = [R.random_layer(rng, dim, H, Dh, ff) for _ in range(2 * depth)]
+    fg = (1 + rng.standard_normal(dim) * 0.02).astype(np.float32)
+    x = rng.standard_normal((B, T, Fb, dim)).astype(np.float32)
+    y = oracle.roformer_stack(x, [oracle.LayerWeights(**w) for w in layers], H, Dh, fg)
+    r = R.stack(x, layers, H, Dh, fg).numpy()
+    assert rel_err(y, r) < 5e-6
+
+
+def test_stack_axis_order_matters(oracle):
+    """Swapping the time and frequency transformers changes the result, so
+    the axis-order pin above is not vacuous."""
+    rng = np.random.default_rng(3)
+    B, T, Fb, dim, H, Dh, ff = 1, 6, 4, 32, 2, 16, 64
+    layers = [R.random_layer(rng, dim, H, Dh, ff) for _ in range(2)]
+    x = rng.standard_normal((B, T, Fb, dim)).astype(np.float32)
+    a = oracle.roformer_stack(x, [oracle.LayerWeights(**w) for w in layers], H, Dh)
+    b = oracle.roformer_stack(x, [oracle.LayerWeights(**w) for w in layers[::-1]], H, Dh)
+    assert rel_err(a, b) > 1e-3
