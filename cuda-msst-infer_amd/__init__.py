@@ -93,7 +93,8 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise MsstError(f"{LIB_PATH} is not built; run build() (hipcc, gfx950)")
-        l = ctypes.CDLL(LIB_PATH)
+        # RTLD_NOW: an unresolved symbol fails here, not at first call.
+        l = ctypes.CDLL(LIB_PATH, mode=os.RTLD_NOW)
         for name, (args, res) in _SIGS.items():
             fn = getattr(l, name)
             fn.argtypes = args

@@ -27,6 +27,8 @@
 // 8 XCDs, so workgroup b is given tile (b % 8) * per_xcd + b / 8 — every XCD
 // walks a contiguous run of the row-major tile grid and the column tiles of
 // a row block (which share the same A rows) run together in one L2.
+#include <stdlib.h>
+
 #include "msst_common.hpp"
 
 namespace msst {
@@ -54,14 +56,135 @@ __device__ __forceinline__ void epilogue_store(float v, int64_t row, int col, in
     out[idx] = (OutT)v;
 }
 
+template <typename T>
+__device__ __forceinline__ f4 ld4(const T* p);
+template <>
+__device__ __forceinline__ f4 ld4<float>(const float* p) { return *reinterpret_cast<const f4*>(p); }
+template <>
+__device__ __forceinline__ f4 ld4<half_t>(const half_t* p) {
+    h4 v = *reinterpret_cast<const h4*>(p);
+    return f4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+template <typename T>
+__device__ __forceinline__ void st4(T* p, f4 v);
+template <>
+__device__ __forceinline__ void st4<float>(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
+template <>
+__device__ __forceinline__ void st4<half_t>(half_t* p, f4 v) {
+    *reinterpret_cast<h4*>(p) = h4{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+}
+
+// Largest divisor IP of MI whose IP*32 x WN fp32 block fits a wave's
+// REGION floats of LDS.
+template <int MI, int WN, int REGION>
+constexpr int pick_ip() {
+    int ip = MI;
+    while (ip > 1 && (ip * 32 * WN > REGION || MI % ip != 0)) --ip;
+    return ip;
+}
+
+// Epilogue through LDS.  A wave's (MI*32) x (NI*32) accumulator block is
+// written to its LDS region IP fragment-rows at a time (static register
+// indices), then read back row-contiguously: each lane owns 4 consecutive
+// columns, so bias is loaded once and global stores are 16-byte (f32) /
+// 8-byte (f16) and row-contiguous.  The read-back runs in batches of U rows
+// per lane: residual loads of the batch first, then its LDS reads, then
+// math and stores — so stores never wait on each other (CDNA counts loads
+// and stores on one vmcnt; a global load inside a rolled loop would make
+// every iteration wait for all earlier stores).  RES is compile-time for
+// the same reason.  All waves run the same trip counts, so the block
+// barriers are uniform.  Caller: LDS free (after a barrier).
+template <int MI, int NI, int IP, bool RES, typename OutT>
+__device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds, int lane,
+                                               int row0, int col0, int M, int N,
+                                               const float* __restrict__ bias, int act,
+                                               const OutT* residual, OutT* out, bool vec) {
+    static_assert(MI % IP == 0, "IP must divide MI");
+    constexpr int WN = NI * 32;
+    constexpr int LPR = WN / 4;    // lanes per row
+    constexpr int RPI = 64 / LPR;  // rows per iteration
+    constexpr int ITERS = IP * 32 / RPI;
+    constexpr int U = ITERS >= 8 ? 8 : ITERS;
+    static_assert(ITERS % U == 0, "batch must divide the row count");
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int rr = lane / LPR, cq = lane % LPR;
+    const int col = col0 + cq * 4;
+    // Wave-uniform: the whole wave tile lies inside N with aligned rows, so
+    // only one of the store paths below ever executes for a wave.
+    const bool full = vec && col0 + WN <= N;
+    f4 bv = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (bias) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = (col + e < N) ? bias[col + e] : 0.0f;
+    }
+#pragma unroll
+    for (int p = 0; p < MI / IP; ++p) {
+#pragma unroll
+        for (int ii = 0; ii < IP; ++ii)
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int r = ii * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                    wlds[r * WN + j * 32 + lrow] = acc[p * IP + ii][j][v];
+                }
+        __syncthreads();
+        const int prow0 = row0 + p * IP * 32;
+#pragma unroll 1
+        for (int it0 = 0; it0 < ITERS; it0 += U) {
+            f4 rv[U];
+            if constexpr (RES) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int grow = prow0 + (it0 + u) * RPI + rr;
+                    const int64_t idx = (int64_t)grow * N + col;
+                    rv[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                    if (grow < M) {
+                        if (full) {
+                            rv[u] = ld4<OutT>(residual + idx);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (col + e < N) rv[u][e] = (float)residual[idx + e];
+                        }
+                    }
+                }
+            }
+            f4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                v[u] = *reinterpret_cast<const f4*>(wlds + ((it0 + u) * RPI + rr) * WN + cq * 4);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int grow = prow0 + (it0 + u) * RPI + rr;
+                if (grow < M) {
+                    f4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = act_apply(v[u][e] + bv[e], act);
+                    if constexpr (RES) o += rv[u];
+                    const int64_t idx = (int64_t)grow * N + col;
+                    if (full) {
+                        st4<OutT>(out + idx, o);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (col + e < N) out[idx + e] = (OutT)o[e];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------------------
 // fp16 MFMA GEMM.  BK = 64 halves (one 128-byte LDS row per tile row).
 // ---------------------------------------------------------------------------
-template <int BM, int BN, bool A_F32, typename OutT>
+template <int BM, int BN, bool A_F32, bool RES, typename OutT>
 __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(
     const void* __restrict__ Aptr, const half_t* __restrict__ W,
     const float* __restrict__ bias, const OutT* residual, OutT* out,
-    int M, int N, int K, int act, int tiles_n, int per_xcd) {
+    int M, int N, int K, int act, int tiles_n, int per_xcd, int vec) {
     constexpr int BK = 64;
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int MI = WM / 32, NI = WN / 32;
@@ -173,18 +296,12 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(
         __syncthreads();
     }
 
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NI; ++j) {
-            const int col = n0 + wn * WN + j * 32 + lrow;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * lhalf + (v & 3);
-                if (row < M && col < N)
-                    epilogue_store<OutT>(acc[i][j][v], row, col, N, bias, act, residual, out);
-            }
-        }
+    constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
+    constexpr int kIP = pick_ip<MI, WN, kRegion>();
+    static_assert(kIP * 32 * WN <= kRegion, "epilogue staging does not fit in LDS");
+    store_tile_lds<MI, NI, kIP, RES, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+                                      lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act, residual,
+                                      out, vec != 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -192,11 +309,11 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(
 // feeds K positions h*16 + s (s = 0..15) of each k-tile: four 16-byte LDS
 // reads per operand fragment.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, bool A_F16, typename OutT>
+template <int BM, int BN, bool A_F16, bool RES, typename OutT>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
     const void* __restrict__ Aptr, const float* __restrict__ W,
     const float* __restrict__ bias, const OutT* residual, OutT* out,
-    int M, int N, int K, int act, int tiles_n, int per_xcd) {
+    int M, int N, int K, int act, int tiles_n, int per_xcd, int vec) {
     constexpr int BK = 32;
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int MI = WM / 32, NI = WN / 32;
@@ -305,18 +422,369 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
         __syncthreads();
     }
 
+    constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
+    constexpr int kIP = pick_ip<MI, WN, kRegion>();
+    static_assert(kIP * 32 * WN <= kRegion, "epilogue staging does not fit in LDS");
+    store_tile_lds<MI, NI, kIP, RES, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+                                      lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act, residual,
+                                      out, vec != 0);
+}
+
+// ---------------------------------------------------------------------------
+// fp16 MFMA GEMM fed by LDS DMA (the fast path: f16 x, f16 W, K % 64 == 0).
+//
+// Tiles move global -> LDS with buffer_load_dwordx4 ... lds: each
+// instruction writes 64 lanes x 16 bytes = 8 tile rows of 128 bytes
+// contiguously, so the XOR swizzle is applied on the source side (lane l
+// fetches logical chunk (l & 7) ^ (l >> 3) of row l >> 3).  No VGPRs stage
+// the tiles and no ds_write is issued.  Rows past M / N are clamped to the
+// last valid row (their results are never stored).  The next k-tile's DMA
+// is issued before the current tile's MFMAs; fragments of k-substep kk+1
+// are read from LDS while the MFMAs of kk run.  One vmcnt wait + barrier
+// per k-tile.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 16-byte-per-lane DMA of buffer bytes [voffset, voffset + 16) into LDS at
+// lds + 16 * lane (lds is wave-uniform).  Offsets at or past `bytes` read
+// zero.  The buffer descriptor type only exists in device code, so kernels
+// reach it through this helper (a kernel naming it loses its host stub).
+__device__ __forceinline__ void dma16(const void* base, int bytes, half_t* lds, uint32_t voffset) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voffset, 0, 0, 0);
+}
+
+template <int BK>
+__device__ __forceinline__ int chunk_swz(int r) {
+    // LDS rows of BK halves = BK/8 chunks of 16 B.  A b128 read is serviced
+    // 16 lanes (256 bytes, 64 banks) at a time; the 16 lanes read the same
+    // logical chunk of 16 consecutive rows, so the XOR must give those rows
+    // 16 distinct 16-byte bank groups: (r >> 1) & 7 for 128-byte rows (odd
+    // rows already sit 32 banks over), (r >> 2) & 3 for 64-byte rows.
+    if constexpr (BK == 64) return ((r >> 1) & 7);
+    else return ((r >> 2) & 3);
+}
+
+// BK = 64 (128-byte LDS rows) or 32 (64-byte rows).  MINB = workgroups per
+// CU the register/LDS budget is sized for: with 256x128 tiles and BK = 32
+// two workgroups share a CU (48 KB LDS, <= 256 registers per lane), so one
+// workgroup's epilogue overlaps the other's main loop instead of every CU
+// storing at the same moment.
+template <int BM, int BN, int BK, int MINB, bool RES, typename OutT>
+__global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
+    const half_t* __restrict__ A, const half_t* __restrict__ W, const float* __restrict__ bias,
+    const OutT* residual, OutT* out, int M, int N, int K, int act, int tiles_n, int per_xcd,
+    int vec) {
+    constexpr int CPR = BK / 8;              // 16-byte chunks per LDS row
+    constexpr int RPD = 64 / CPR;            // rows per 1 KB DMA instruction
+    constexpr int KK = BK / 16;              // MFMA k-substeps per k-tile
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int MI = WM / 32, NI = WN / 32;
+    constexpr int A_INST = BM / RPD / 4;     // DMA instructions per wave per k-tile
+    constexpr int B_INST = BN / RPD / 4;
+    constexpr int STAGE = (BM + BN) * BK;    // halves per LDS buffer
+    static_assert(A_INST >= 1 && B_INST >= 1, "tile too small for the DMA split");
+    __shared__ __attribute__((aligned(16))) half_t lds[2][STAGE];
+
+    int tm, tn;
+    tile_coords(tiles_n, per_xcd, tm, tn, ((M + BM - 1) / BM) * tiles_n);
+    if (tm < 0) return;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wid = tid >> 6;
+    const int wm = wid >> 1, wn = wid & 1;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+
+    const int a_bytes = M * K * 2, b_bytes = N * K * 2;
+    const int sub_row = lane / CPR;
+    uint32_t aoff[A_INST], boff[B_INST];
+#pragma unroll
+    for (int i = 0; i < A_INST; ++i) {
+        const int rl = (wid * A_INST + i) * RPD + sub_row;  // row within the tile
+        const int lchunk = (lane % CPR) ^ chunk_swz<BK>(rl);
+        const int r = min(m0 + rl, M - 1);
+        aoff[i] = (uint32_t)(r * K + lchunk * 8) * 2u;
+    }
+#pragma unroll
+    for (int i = 0; i < B_INST; ++i) {
+        const int rl = (wid * B_INST + i) * RPD + sub_row;
+        const int lchunk = (lane % CPR) ^ chunk_swz<BK>(rl);
+        const int r = min(n0 + rl, N - 1);
+        boff[i] = (uint32_t)(r * K + lchunk * 8) * 2u;
+    }
+    auto issue = [&](int k0, int buf) {
+        half_t* As = lds[buf];
+        half_t* Bs = lds[buf] + BM * BK;
+        const uint32_t kb = (uint32_t)k0 * 2u;
+#pragma unroll
+        for (int i = 0; i < A_INST; ++i)
+            dma16(A, a_bytes, As + (wid * A_INST + i) * 512, aoff[i] + kb);
+#pragma unroll
+        for (int i = 0; i < B_INST; ++i)
+            dma16(W, b_bytes, Bs + (wid * B_INST + i) * 512, boff[i] + kb);
+    };
+
+    f16x acc[MI][NI];
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < NI; ++j) {
-            const int col = n0 + wn * WN + j * 32 + lrow;
+        for (int j = 0; j < NI; ++j) acc[i][j] = f16x{};
+
+    const int KT = K / BK;
+    issue(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        // Branch-free prefetch (one basic block per k-tile for the
+        // scheduler): the last iteration re-fetches the last tile into the
+        // idle buffer, which nothing reads.
+        issue(min(kt + 1, KT - 1) * BK, cur ^ 1);
+        const half_t* As = lds[cur];
+        const half_t* Bs = lds[cur] + BM * BK;
+        h8 af[KK][MI], bf[KK][NI];
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * lhalf + (v & 3);
-                if (row < M && col < N)
-                    epilogue_store<OutT>(acc[i][j][v], row, col, N, bias, act, residual, out);
+        for (int kk = 0; kk < KK; ++kk) {
+            const int c = kk * 2 + lhalf;
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int r = wm * WM + i * 32 + lrow;
+                af[kk][i] = *reinterpret_cast<const h8*>(As + r * BK + ((c ^ chunk_swz<BK>(r)) << 3));
+            }
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                const int r = wn * WN + j * 32 + lrow;
+                bf[kk][j] = *reinterpret_cast<const h8*>(Bs + r * BK + ((c ^ chunk_swz<BK>(r)) << 3));
             }
         }
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j)
+                    acc[i][j] = mfma32x32x16(af[kk][i], bf[kk][j], acc[i][j]);
+        // Interleave the fragment reads with the MFMAs; keep the MFMAs of
+        // this k-tile ahead of the end-of-tile wait.
+        __builtin_amdgcn_iglp_opt(1);
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+
+    constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
+    constexpr int kIP = pick_ip<MI, WN, kRegion>();
+    static_assert(kIP * 32 * WN <= kRegion, "epilogue staging does not fit in LDS");
+    store_tile_lds<MI, NI, kIP, RES, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+                                           lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act,
+                                           residual, out, vec != 0);
+}
+
+// ---------------------------------------------------------------------------
+// Persistent fp16 GEMM (the production fast path).
+//
+// One workgroup per CU walks a list of output tiles.  Its k-tiles form one
+// continuous stream across tiles: a 3-slot LDS ring (BK = 32) is filled by
+// LDS DMA two k-tiles ahead of the MFMAs, so while tile t's epilogue runs
+// (through a separate LDS staging area) the first k-tiles of tile t+1 are
+// already in flight.  Measured on MI355X: L2 -> LDS streaming saturates at
+// ~75-95 GB/s per CU whatever the depth, so a 256x256 tile (1/128 byte per
+// flop) sits near that limit at full MFMA rate; hiding the epilogue behind
+// the next tile's loads is what the persistent form buys.
+//
+// Ring rows are 64 bytes (4 chunks of 16 B); chunk c of row r is stored at
+// c ^ ((r >> 1) & 3), conflict-free for the 8-row groups of a b128 read.
+// A DMA instruction fills 16 rows: lane l takes row l >> 2, physical chunk
+// l & 3.
+// ---------------------------------------------------------------------------
+template <typename OutT>
+__device__ __forceinline__ void st16(OutT* p, const float* v);
+template <>
+__device__ __forceinline__ void st16<float>(float* p, const float* v) {
+    *reinterpret_cast<f4*>(p) = f4{v[0], v[1], v[2], v[3]};
+}
+template <>
+__device__ __forceinline__ void st16<half_t>(half_t* p, const float* v) {
+    h8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (half_t)v[e];
+    *reinterpret_cast<h8*>(p) = h;
+}
+
+// Epilogue with 16-byte stores: one 32-row fragment row at a time through
+// the wave's staging area (32 x WN floats), E = 16 / sizeof(OutT) columns
+// per lane.  No global loads: the persistent kernel serves GEMMs without a
+// residual, so stores are never waited on inside the epilogue.
+template <int MI, int NI, typename OutT>
+__device__ __forceinline__ void store_tile16(f16x (&acc)[MI][NI], float* stg, int lane, int row0,
+                                             int col0, int M, int N,
+                                             const float* __restrict__ bias, int act, OutT* out,
+                                             bool vec) {
+    constexpr int WN = NI * 32;
+    constexpr int E = 16 / (int)sizeof(OutT);
+    constexpr int LPR = WN / E;
+    constexpr int RPI = 64 / LPR;
+    constexpr int ITERS = 32 / RPI;
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int rr = lane / LPR, cq = lane % LPR;
+    const int col = col0 + cq * E;
+    const bool full = vec && col0 + WN <= N;  // wave-uniform
+    float bv[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) bv[e] = (bias && col + e < N) ? bias[col + e] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                stg[(8 * (v >> 2) + 4 * lh + (v & 3)) * WN + j * 32 + lrow] = acc[i][j][v];
+        __syncthreads();
+        const int irow0 = row0 + i * 32;
+#pragma unroll 2
+        for (int it = 0; it < ITERS; ++it) {
+            const int r = it * RPI + rr;
+            const int grow = irow0 + r;
+            float o[E];
+#pragma unroll
+            for (int e = 0; e < E; e += 4) {
+                f4 t = *reinterpret_cast<const f4*>(stg + r * WN + cq * E + e);
+                o[e] = t[0]; o[e + 1] = t[1]; o[e + 2] = t[2]; o[e + 3] = t[3];
+            }
+#pragma unroll
+            for (int e = 0; e < E; ++e) o[e] = act_apply(o[e] + bv[e], act);
+            if (grow < M) {
+                const int64_t idx = (int64_t)grow * N + col;
+                if (full) {
+                    st16<OutT>(out + idx, o);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < E; ++e)
+                        if (col + e < N) out[idx + e] = (OutT)o[e];
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int BM, int BN, typename OutT>
+__global__ __launch_bounds__(kThreads) void gemm_f16_persist_kernel(
+    const half_t* __restrict__ A, const half_t* __restrict__ W, const float* __restrict__ bias,
+    OutT* out, int M, int N, int K, int act, int tiles_n, int n_tiles, int per_xcd, int vec) {
+    constexpr int BK = 32, NSTG = 3;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int MI = WM / 32, NI = WN / 32;
+    constexpr int A_INST = BM * BK * 2 / 1024 / 4;  // 1 KB DMA instructions per wave per stage
+    constexpr int B_INST = BN * BK * 2 / 1024 / 4;
+    constexpr int INST = A_INST + B_INST;
+    constexpr int STAGE = (BM + BN) * BK;  // halves
+    static_assert(A_INST >= 1 && B_INST >= 1, "tile too small");
+    __shared__ __attribute__((aligned(16))) half_t ring[NSTG * STAGE];
+    __shared__ __attribute__((aligned(16))) float stg[4 * 32 * WN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wid = tid >> 6;
+    const int wm = wid >> 1, wn = wid & 1;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+
+    // This workgroup's tiles: XCD x owns the contiguous run
+    // [x*per_xcd, (x+1)*per_xcd) of the row-major tile grid; the nq
+    // workgroups on it take every nq-th tile of the run.
+    const int x = blockIdx.x & 7, q = blockIdx.x >> 3, nq = gridDim.x >> 3;
+    const int t_begin = x * per_xcd;
+    const int t_end = min(n_tiles, t_begin + per_xcd);
+    const int n_local = t_begin + q < t_end ? (t_end - t_begin - q + nq - 1) / nq : 0;
+    const int KT = K / BK;
+    const int G = n_local * KT;
+    if (G == 0) return;
+
+    const int a_bytes = M * K * 2, b_bytes = N * K * 2;
+    const int sub_row = lane >> 2;
+    const int lchunk = (lane & 3) ^ ((lane >> 3) & 3);
+
+    auto issue = [&](int g) {
+        const int t = t_begin + q + (g / KT) * nq;
+        const int kt = g - (g / KT) * KT;
+        const int tm = t / tiles_n, tn = t - (t / tiles_n) * tiles_n;
+        half_t* As = ring + (g % NSTG) * STAGE;
+        half_t* Bs = As + BM * BK;
+        const int kofs = kt * BK + lchunk * 8;
+#pragma unroll
+        for (int i = 0; i < A_INST; ++i) {
+            const int r = min(tm * BM + (wid * A_INST + i) * 16 + sub_row, M - 1);
+            dma16(A, a_bytes, As + (wid * A_INST + i) * 512, (uint32_t)(r * K + kofs) * 2u);
+        }
+#pragma unroll
+        for (int i = 0; i < B_INST; ++i) {
+            const int r = min(tn * BN + (wid * B_INST + i) * 16 + sub_row, N - 1);
+            dma16(W, b_bytes, Bs + (wid * B_INST + i) * 512, (uint32_t)(r * K + kofs) * 2u);
+        }
+    };
+
+    issue(0);
+    if (G > 1) issue(1);
+
+    for (int jt = 0; jt < n_local; ++jt) {
+        f16x acc[MI][NI];
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) acc[i][j] = f16x{};
+
+        // The k-loop of one tile: the accumulators stay in AGPRs for its
+        // whole length (an epilogue inside the loop body would make the
+        // compiler shuttle them through VGPRs every iteration).
+        for (int kt = 0; kt < KT; ++kt) {
+            const int g = jt * KT + kt;
+            // Stage g must have landed.  Newer outstanding work: DMA g+1
+            // and, at a tile start, the previous tile's epilogue stores
+            // (waited for as well).
+            if (g + 1 < G && kt != 0) {
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(INST) : "memory");
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            __syncthreads();
+            if (g + 2 < G) issue(g + 2);  // into the slot consumed at g-1
+            const half_t* As = ring + (g % NSTG) * STAGE;
+            const half_t* Bs = As + BM * BK;
+            h8 af[2][MI], bf[2][NI];
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int c = kk * 2 + lhalf;
+#pragma unroll
+                for (int i = 0; i < MI; ++i) {
+                    const int r = wm * WM + i * 32 + lrow;
+                    af[kk][i] =
+                        *reinterpret_cast<const h8*>(As + r * BK + ((c ^ ((r >> 1) & 3)) << 3));
+                }
+#pragma unroll
+                for (int j = 0; j < NI; ++j) {
+                    const int r = wn * WN + j * 32 + lrow;
+                    bf[kk][j] =
+                        *reinterpret_cast<const h8*>(Bs + r * BK + ((c ^ ((r >> 1) & 3)) << 3));
+                }
+            }
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NI; ++j)
+                        acc[i][j] = mfma32x32x16(af[kk][i], bf[kk][j], acc[i][j]);
+            __builtin_amdgcn_iglp_opt(1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        const int t = t_begin + q + jt * nq;
+        const int tm = t / tiles_n, tn = t - (t / tiles_n) * tiles_n;
+        store_tile16<MI, NI, OutT>(acc, stg + wid * 32 * WN, lane, tm * BM + wm * WM,
+                                   tn * BN + wn * WN, M, N, bias, act, out, vec != 0);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -386,19 +854,89 @@ int num_xcd_slots(int64_t tiles, int& per_xcd) {
     return per_xcd * 8;
 }
 
+template <typename OutT>
+int vec_flag(const OutT* res, const OutT* out, int N) {
+    return (N % 4 == 0 && aligned(out, 4 * sizeof(OutT)) && aligned(res, 4 * sizeof(OutT))) ? 1
+                                                                                            : 0;
+}
+
 template <int BM, int BN, typename OutT>
 int launch_f16(const void* x, bool x_f32, const half_t* w, const float* bias,
                const OutT* res, OutT* out, int M, int N, int K, int act, hipStream_t s) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int per_xcd;
     int grid = num_xcd_slots((int64_t)tiles_m * tiles_n, per_xcd);
-    if (x_f32)
-        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, true, OutT>), dim3(grid), dim3(kThreads), 0, s,
-                           x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd);
-    else
-        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, false, OutT>), dim3(grid), dim3(kThreads), 0, s,
-                           x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd);
+    const int vec = vec_flag(res, out, N);
+#define MSST_L16(AF, RS)                                                                        \
+    hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, AF, RS, OutT>), dim3(grid), dim3(kThreads), 0, s, \
+                       x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd, vec)
+    if (x_f32) {
+        if (res) MSST_L16(true, true); else MSST_L16(true, false);
+    } else {
+        if (res) MSST_L16(false, true); else MSST_L16(false, false);
+    }
+#undef MSST_L16
     return check_launch("gemm_f16_kernel");
+}
+
+template <int BM, int BN, int BK, int MINB, typename OutT>
+int launch_f16_dma(const half_t* x, const half_t* w, const float* bias, const OutT* res,
+                   OutT* out, int M, int N, int K, int act, hipStream_t s) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    int per_xcd;
+    int grid = num_xcd_slots((int64_t)tiles_m * tiles_n, per_xcd);
+    const int vec = vec_flag(res, out, N);
+    if (res)
+        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, MINB, true, OutT>), dim3(grid),
+                           dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act, tiles_n,
+                           per_xcd, vec);
+    else
+        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, MINB, false, OutT>), dim3(grid),
+                           dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act, tiles_n,
+                           per_xcd, vec);
+    return check_launch("gemm_f16_dma_kernel");
+}
+
+// MSST_GEMM_VARIANT selects among the exact fp16 kernels for A/B timing:
+// 0 = persistent, 1 = one 256x256 / 256x128 tile per workgroup (BK 64),
+// 2 = 256x128 tiles, BK 32, two workgroups per CU (default).
+int gemm_variant() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("MSST_GEMM_VARIANT");
+        v = (e && e[0] >= '0' && e[0] <= '2') ? e[0] - '0' : 2;
+    }
+    return v;
+}
+
+int cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    return cus;
+}
+
+template <int BM, int BN, typename OutT>
+int launch_f16_persist(const half_t* x, const half_t* w, const float* bias, OutT* out, int M,
+                       int N, int K, int act, hipStream_t s) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const int n_tiles = tiles_m * tiles_n;
+    const int per_xcd = (n_tiles + 7) / 8;
+    int nq = cu_count() / 8;
+    if (nq < 1) nq = 1;
+    if (nq > per_xcd) nq = per_xcd;
+    const int grid = 8 * nq;
+    hipLaunchKernelGGL((gemm_f16_persist_kernel<BM, BN, OutT>), dim3(grid), dim3(kThreads), 0, s,
+                       x, w, bias, out, M, N, K, act, tiles_n, n_tiles, per_xcd,
+                       vec_flag<OutT>(nullptr, out, N));
+    return check_launch("gemm_f16_persist_kernel");
 }
 
 template <int BM, int BN, typename OutT>
@@ -407,12 +945,16 @@ int launch_f32(const void* x, bool x_f16, const float* w, const float* bias,
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int per_xcd;
     int grid = num_xcd_slots((int64_t)tiles_m * tiles_n, per_xcd);
-    if (x_f16)
-        hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, true, OutT>), dim3(grid), dim3(kThreads), 0, s,
-                           x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd);
-    else
-        hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, false, OutT>), dim3(grid), dim3(kThreads), 0, s,
-                           x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd);
+    const int vec = vec_flag(res, out, N);
+#define MSST_L32(AH, RS)                                                                        \
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, AH, RS, OutT>), dim3(grid), dim3(kThreads), 0, s, \
+                       x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd, vec)
+    if (x_f16) {
+        if (res) MSST_L32(true, true); else MSST_L32(true, false);
+    } else {
+        if (res) MSST_L32(false, true); else MSST_L32(false, false);
+    }
+#undef MSST_L32
     return check_launch("gemm_f32_kernel");
 }
 
@@ -451,6 +993,28 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
                      : launch_small<half_t, float, OutT>(x, w, bias, res, o, M, n, k, act, s);
     }
     if (w_dtype == MSST_F16) {
+        // LDS-DMA fast path: f16 operands, whole 64-wide k-tiles, 32-bit
+        // buffer offsets.
+        const bool dma_ok = !x_f32 && K % 64 == 0 && aligned(x, 16) && aligned(w, 16) &&
+                            (M + 256) * K * 2 < ((int64_t)1 << 31) &&
+                            (N + 256) * K * 2 < ((int64_t)1 << 31);
+        if (dma_ok) {
+            const half_t* xh = reinterpret_cast<const half_t*>(x);
+            const half_t* wh = reinterpret_cast<const half_t*>(w);
+            const int variant = gemm_variant();
+            if (variant == 0 && res == nullptr) {
+                if (N >= 1024)
+                    return launch_f16_persist<256, 256, OutT>(xh, wh, bias, o, m, n, k, act, s);
+                return launch_f16_persist<256, 128, OutT>(xh, wh, bias, o, m, n, k, act, s);
+            }
+            if (variant == 1) {
+                if (N >= 1024)
+                    return launch_f16_dma<256, 256, 64, 1, OutT>(xh, wh, bias, res, o, m, n, k, act,
+                                                                 s);
+                return launch_f16_dma<256, 128, 64, 1, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
+            }
+            return launch_f16_dma<256, 128, 32, 2, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
+        }
         const bool vec_ok = (K % 8 == 0) && aligned(x, 16) && aligned(w, 16);
         if (!vec_ok)
             return x_f32 ? launch_small<float, half_t, OutT>(x, w, bias, res, o, M, n, k, act, s)
