@@ -466,12 +466,12 @@ __device__ __forceinline__ int chunk_swz(int r) {
     else return ((r >> 2) & 3);
 }
 
-// BK = 64 (128-byte LDS rows) or 32 (64-byte rows).  MINB = workgroups per
-// CU the register/LDS budget is sized for: with 256x128 tiles and BK = 32
-// two workgroups share a CU (48 KB LDS, <= 256 registers per lane), so one
-// workgroup's epilogue overlaps the other's main loop instead of every CU
-// storing at the same moment.
-template <int BM, int BN, int BK, int MINB, bool RES, typename OutT>
+// BK = 64 (128-byte LDS rows) or 32 (64-byte rows).  NSTG = LDS ring
+// stages: the DMA of k-tile t + NSTG - 1 is issued while tile t computes,
+// so a load has NSTG - 1 k-tiles of MFMA time to land.  MINB = workgroups
+// per CU the register/LDS budget is sized for (two for 256x128 tiles, so
+// one workgroup's epilogue overlaps the other's main loop).
+template <int BM, int BN, int BK, int NSTG, int MINB, bool RES, typename OutT>
 __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
     const half_t* __restrict__ A, const half_t* __restrict__ W, const float* __restrict__ bias,
     const OutT* residual, OutT* out, int M, int N, int K, int act, int tiles_n, int per_xcd,
@@ -485,7 +485,8 @@ __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
     constexpr int B_INST = BN / RPD / 4;
     constexpr int STAGE = (BM + BN) * BK;    // halves per LDS buffer
     static_assert(A_INST >= 1 && B_INST >= 1, "tile too small for the DMA split");
-    __shared__ __attribute__((aligned(16))) half_t lds[2][STAGE];
+    static_assert(NSTG >= 2 && (NSTG - 2) * (A_INST + B_INST) <= 63, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) half_t lds[NSTG][STAGE];
 
     int tm, tn;
     tile_coords(tiles_n, per_xcd, tm, tn, ((M + BM - 1) / BM) * tiles_n);
@@ -514,17 +515,16 @@ __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
         const int r = min(n0 + rl, N - 1);
         boff[i] = (uint32_t)(r * K + lchunk * 8) * 2u;
     }
-    auto issue = [&](int k0, int buf) {
-        half_t* As = lds[buf];
-        half_t* Bs = lds[buf] + BM * BK;
+    // DMA instruction `idx` (0 .. A_INST+B_INST-1) of the k-tile at k0.
+    auto issue_one = [&](int idx, int k0, int buf) {
         const uint32_t kb = (uint32_t)k0 * 2u;
-#pragma unroll
-        for (int i = 0; i < A_INST; ++i)
-            dma16(A, a_bytes, As + (wid * A_INST + i) * 512, aoff[i] + kb);
-#pragma unroll
-        for (int i = 0; i < B_INST; ++i)
-            dma16(W, b_bytes, Bs + (wid * B_INST + i) * 512, boff[i] + kb);
+        if (idx < A_INST)
+            dma16(A, a_bytes, lds[buf] + (wid * A_INST + idx) * 512, aoff[idx] + kb);
+        else
+            dma16(W, b_bytes, lds[buf] + BM * BK + (wid * B_INST + idx - A_INST) * 512,
+                  boff[idx - A_INST] + kb);
     };
+    constexpr int INST = A_INST + B_INST;
 
     f16x acc[MI][NI];
 #pragma unroll
@@ -533,21 +533,32 @@ __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
         for (int j = 0; j < NI; ++j) acc[i][j] = f16x{};
 
     const int KT = K / BK;
-    issue(0, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    // Prologue: k-tiles 0 .. NSTG-2 (clamped: short K re-fetches the last
+    // tile, keeping the per-stage instruction count fixed for vmcnt).
+#pragma unroll
+    for (int st = 0; st < NSTG - 1; ++st)
+#pragma unroll
+        for (int idx = 0; idx < INST; ++idx) issue_one(idx, min(st, KT - 1) * BK, st);
 
+    // Issue order of one k-tile, pinned with scheduling fences: fragments of
+    // substep kk+1 are read while the MFMAs of kk run, and the DMA of k-tile
+    // kt + NSTG - 1 is spread between MFMA row groups — issued as one burst
+    // it stalls the wave on a full load queue before its first MFMA.
+    constexpr int GROUPS = KK * MI;                      // MFMA row groups per k-tile
+    constexpr int PER_G = (INST + GROUPS - 1) / GROUPS;  // DMA instructions per group
     for (int kt = 0; kt < KT; ++kt) {
-        const int cur = kt & 1;
-        // Branch-free prefetch (one basic block per k-tile for the
-        // scheduler): the last iteration re-fetches the last tile into the
-        // idle buffer, which nothing reads.
-        issue(min(kt + 1, KT - 1) * BK, cur ^ 1);
+        // k-tile kt has landed once at most the NSTG-2 newer stages remain.
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTG - 2) * INST) : "memory");
+        __syncthreads();
+        const int cur = kt % NSTG;
+        const int nslot = (kt + NSTG - 1) % NSTG;  // the slot consumed at kt - 1
+        // Past the end the DMA re-fetches the last k-tile into a slot that
+        // is never read again (keeps every iteration's count equal).
+        const int knext = min(kt + NSTG - 1, KT - 1) * BK;
         const half_t* As = lds[cur];
         const half_t* Bs = lds[cur] + BM * BK;
         h8 af[KK][MI], bf[KK][NI];
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
+        auto load_frags = [&](int kk) {
             const int c = kk * 2 + lhalf;
 #pragma unroll
             for (int i = 0; i < MI; ++i) {
@@ -559,21 +570,29 @@ __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
                 const int r = wn * WN + j * 32 + lrow;
                 bf[kk][j] = *reinterpret_cast<const h8*>(Bs + r * BK + ((c ^ chunk_swz<BK>(r)) << 3));
             }
-        }
+        };
+        load_frags(0);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk)
+        for (int kk = 0; kk < KK; ++kk) {
+            if (kk + 1 < KK) load_frags(kk + 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < MI; ++i)
+            for (int i = 0; i < MI; ++i) {
 #pragma unroll
                 for (int j = 0; j < NI; ++j)
                     acc[i][j] = mfma32x32x16(af[kk][i], bf[kk][j], acc[i][j]);
-        // Interleave the fragment reads with the MFMAs; keep the MFMAs of
-        // this k-tile ahead of the end-of-tile wait.
-        __builtin_amdgcn_iglp_opt(1);
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+#pragma unroll
+                for (int u = 0; u < PER_G; ++u) {
+                    const int idx = (kk * MI + i) * PER_G + u;
+                    if (idx < INST) issue_one(idx, knext, nslot);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
 
     constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
     constexpr int kIP = pick_ip<MI, WN, kRegion>();
@@ -879,7 +898,7 @@ int launch_f16(const void* x, bool x_f32, const half_t* w, const float* bias,
     return check_launch("gemm_f16_kernel");
 }
 
-template <int BM, int BN, int BK, int MINB, typename OutT>
+template <int BM, int BN, int BK, int NSTG, int MINB, typename OutT>
 int launch_f16_dma(const half_t* x, const half_t* w, const float* bias, const OutT* res,
                    OutT* out, int M, int N, int K, int act, hipStream_t s) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -887,24 +906,26 @@ int launch_f16_dma(const half_t* x, const half_t* w, const float* bias, const Ou
     int grid = num_xcd_slots((int64_t)tiles_m * tiles_n, per_xcd);
     const int vec = vec_flag(res, out, N);
     if (res)
-        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, MINB, true, OutT>), dim3(grid),
+        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, true, OutT>), dim3(grid),
                            dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act, tiles_n,
                            per_xcd, vec);
     else
-        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, MINB, false, OutT>), dim3(grid),
+        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, false, OutT>), dim3(grid),
                            dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act, tiles_n,
                            per_xcd, vec);
     return check_launch("gemm_f16_dma_kernel");
 }
 
 // MSST_GEMM_VARIANT selects among the exact fp16 kernels for A/B timing:
-// 0 = persistent, 1 = one 256x256 / 256x128 tile per workgroup (BK 64),
-// 2 = 256x128 tiles, BK 32, two workgroups per CU (default).
+// 0 = persistent; 1 = 256x256 (N >= 1024) / 256x128 tiles, four BK-32
+// stages; 2 = 256x128 tiles, three BK-32 stages, two workgroups per CU
+// (default: the second workgroup's main loop hides the first one's
+// epilogue); 3 = 256x256 / 256x128 tiles, two BK-64 stages.
 int gemm_variant() {
     static int v = -1;
     if (v < 0) {
         const char* e = getenv("MSST_GEMM_VARIANT");
-        v = (e && e[0] >= '0' && e[0] <= '2') ? e[0] - '0' : 2;
+        v = (e && e[0] >= '0' && e[0] <= '3') ? e[0] - '0' : 2;
     }
     return v;
 }
@@ -1009,11 +1030,19 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
             }
             if (variant == 1) {
                 if (N >= 1024)
-                    return launch_f16_dma<256, 256, 64, 1, OutT>(xh, wh, bias, res, o, m, n, k, act,
-                                                                 s);
-                return launch_f16_dma<256, 128, 64, 1, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
+                    return launch_f16_dma<256, 256, 32, 4, 1, OutT>(xh, wh, bias, res, o, m, n, k,
+                                                                    act, s);
+                return launch_f16_dma<256, 128, 32, 4, 1, OutT>(xh, wh, bias, res, o, m, n, k, act,
+                                                                s);
             }
-            return launch_f16_dma<256, 128, 32, 2, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
+            if (variant == 3) {
+                if (N >= 1024)
+                    return launch_f16_dma<256, 256, 64, 2, 1, OutT>(xh, wh, bias, res, o, m, n, k,
+                                                                    act, s);
+                return launch_f16_dma<256, 128, 64, 2, 1, OutT>(xh, wh, bias, res, o, m, n, k, act,
+                                                                s);
+            }
+            return launch_f16_dma<256, 128, 32, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
         }
         const bool vec_ok = (K % 8 == 0) && aligned(x, 16) && aligned(w, 16);
         if (!vec_ok)
