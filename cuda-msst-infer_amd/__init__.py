@@ -64,6 +64,8 @@ _SIGS = {
     "msst_status_string": ([_int], ctypes.c_char_p),
     "msst_last_error": ([], ctypes.c_char_p),
     "msst_linear": ([_vp, _int, _vp, _int, _vp, _vp, _vp, _int, _i64, _i64, _i64, _int, _vp], _int),
+    "msst_linear_rope": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64,
+                          _i64, _vp], _int),
     "msst_rms_norm": ([_vp, _int, _vp, _f, _vp, _int, _i64, _i64, _vp], _int),
     "msst_rms_norm_gate": ([_vp, _int, _vp, _f, _vp, _int, _vp, _int, _vp, _vp, _i64, _i64,
                             _int, _vp], _int),
@@ -142,6 +144,21 @@ def linear(x, w, bias=None, act="none", residual=None, out=None, out_dtype=None)
         out = torch.empty(*x.shape[:-1], N, dtype=od, device=x.device)
     check(lib().msst_linear(_ptr(x), _dt(x), _ptr(w), _dt(w), _ptr(bias), _ptr(residual),
                             _ptr(out), _dt(out), M, K, N, ACT[act], _stream()), "msst_linear")
+    return out
+
+
+def linear_rope(x, w, cos, sin, rope_cols, dim_head, pos_div, pos_mod, bias=None, out=None):
+    """fp16 x . w^T (+ bias) with RoPE on columns [0, rope_cols); row r is at
+    position (r // pos_div) % pos_mod of the [pos_mod, dim_head/2] tables."""
+    import torch
+    K = x.shape[-1]
+    N = w.shape[0]
+    M = x.numel() // K
+    if out is None:
+        out = torch.empty(*x.shape[:-1], N, dtype=torch.float16, device=x.device)
+    check(lib().msst_linear_rope(_ptr(x), _ptr(w), _ptr(bias), _ptr(out), M, K, N, _ptr(cos),
+                                 _ptr(sin), rope_cols, dim_head, pos_div, pos_mod, _stream()),
+          "msst_linear_rope")
     return out
 
 

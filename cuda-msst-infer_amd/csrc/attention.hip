@@ -322,6 +322,243 @@ __global__ __launch_bounds__(256) void attn_f16_kernel(AttnParams p) {
 }
 
 // ===========================================================================
+// fp16 with q/k already rotated (no RoPE tables): K and V by LDS DMA
+// ===========================================================================
+// Each 64-key block lands in LDS as two [64 rows][128 B] tiles in token
+// layout, written by buffer_load ... lds (no VGPR staging, no VALU).
+//   K fragments (A of S^T = K . Q^T) are 16-byte row reads; chunk c of row r
+//   sits at c ^ ((r >> 1) & 7), so the 16 rows one b128 pass serves hit
+//   distinct banks.
+//   V^T fragments (A of O^T += V^T . P^T) come from ds_read_b64_tr_b16:
+//   within each 16-lane group, output lane j element e is element j % 4 of
+//   the 8 bytes read by lane 4e + j / 4.  Lane s of the group points at row
+//   key0 + s / 4, columns d0 + 4 (s % 4) .. + 3, so lane j receives keys
+//   key0 .. key0 + 3 of column d0 + j: the transposed fragment, straight
+//   from the token-layout tile.  Chunk c of V row r sits at
+//   c ^ (4 ((r >> 1) & 1)): the 4 rows x 4 chunks of one half-wave read
+//   then map to distinct banks.
+// Softmax: the score scale folds into the FMA feeding v_exp_f32
+// (s * c - m * c, c = scale * log2 e).  The running max only moves when a
+// block's max exceeds it by more than 8 (log2 units): most blocks skip the
+// rescale of O, and P stays <= 2^8 (exact range for fp16).  Row sums add the
+// fp16 P values the PV MFMA consumes (v_dot2 against 1.0), so numerator and
+// denominator see the same rounding.
+// HPW = 1: 4 waves x 64 queries of one (sequence, head) share double-
+// buffered K/V blocks, each wave DMAs 16 of the 64 rows.  HPW = 4 (<= 64
+// keys): each wave owns one head and DMAs its own single block.
+typedef short s4_t __attribute__((__vector_size__(4 * sizeof(short))));
+typedef __attribute__((address_space(3))) s4_t lds_s4_t;
+
+__device__ __forceinline__ h4 lds_read_tr16(const half_t* ptr) {
+    const s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)(const_cast<half_t*>(ptr)));
+    return __builtin_bit_cast(h4, v);
+}
+
+constexpr float kRescaleLog2 = 8.0f;
+
+template <int HPW>
+__global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
+    constexpr int WPH = 4 / HPW;
+    constexpr int NSLOT = HPW == 1 ? 2 : 4;
+    constexpr int SLOT = 2 * kKB * kD;          // halves: K tile, then V tile
+    constexpr int ROWS_W = HPW == 1 ? 16 : 64;  // block rows one wave DMAs
+    __shared__ __attribute__((aligned(16))) half_t lds[NSLOT * SLOT];
+
+    int64_t item;
+    work_item(p, item);
+    if (item >= p.total_items) return;
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int head_local = w / WPH, qsub = w % WPH;
+    const int head_groups = (p.H + HPW - 1) / HPW;
+    const int qt_idx = (int)(item % p.qtiles);
+    const int64_t sh = item / p.qtiles;
+    const int hg = (int)(sh % head_groups);
+    const int64_t seq = sh / head_groups;
+    const int h = hg * HPW + head_local;
+    const bool head_ok = h < p.H;  // always true for HPW = 1
+    const int q0 = (qt_idx * WPH + qsub) * 64;
+    const bool wave_active = head_ok && q0 < p.n_q;
+
+    // ---- Q operand (B of S^T), held for the whole loop.
+    const half_t* qb = reinterpret_cast<const half_t*>(p.q);
+    h8 qf[2][4];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + qt * 32 + lrow;
+        const bool ok = wave_active && qi < p.n_q;
+        const half_t* row = qb + (ok ? tok_q(p, seq, qi) * p.ld_in + h * p.head_in : 0);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+            qf[qt][kk] = ok ? *reinterpret_cast<const h8*>(row + kk * 16 + lh * 8) : h8{};
+    }
+
+    // ---- K/V DMA.  Rows past the sequence re-read its last key (masked in
+    // the scores, and finite, so P = 0 times V adds exactly 0).
+    const int64_t base_off = head_ok ? tok_k(p, seq, 0) * p.ld_in + h * p.head_in : 0;
+    const half_t* kbase = reinterpret_cast<const half_t*>(p.k) + base_off;
+    const half_t* vbase = reinterpret_cast<const half_t*>(p.v) + base_off;
+    const uint32_t rsb = (uint32_t)(p.k_pos * p.ld_in * 2);  // bytes between keys
+    const int span = (int)((p.n_k - 1) * rsb) + kD * 2;
+    const int row0w = HPW == 1 ? w * ROWS_W : 0;
+    const int sub = lane >> 3, pch = lane & 7;
+    auto slot_ptr = [&](int kb) -> half_t* {
+        return lds + (HPW == 1 ? (kb & 1) : head_local) * SLOT;
+    };
+    auto issue = [&](int kb) {
+        half_t* Ks = slot_ptr(kb);
+        half_t* Vs = Ks + kKB * kD;
+#pragma unroll
+        for (int i = 0; i < ROWS_W / 8; ++i) {
+            const int r = row0w + i * 8 + sub;
+            const uint32_t ro = (uint32_t)min(kb * kKB + r, p.n_k - 1) * rsb;
+            dma16(kbase, span, Ks + (row0w + i * 8) * kD, ro + ((pch ^ ((r >> 1) & 7)) << 4));
+            dma16(vbase, span, Vs + (row0w + i * 8) * kD,
+                  ro + ((pch ^ (((r >> 1) & 1) << 2)) << 4));
+        }
+    };
+
+    // Per-lane parts of the fragment addresses.
+    const int kr_sw = (lrow >> 1) & 7;
+    const int g = lane >> 4, j16 = lane & 15;
+    const int vrow = 4 * (g >> 1) + (j16 >> 2);  // row within an 8-key group
+    const int vsw = ((vrow >> 1) & 1) << 2;
+    const int vch = 2 * (g & 1) + ((j16 & 3) >> 1);
+    const int vsub = (j16 & 1) * 4;
+    int voff[2];
+#pragma unroll
+    for (int dm = 0; dm < 2; ++dm) voff[dm] = vrow * kD + (((4 * dm + vch) ^ vsw) << 3) + vsub;
+
+    f16x o[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) o[a][b] = f16x{};
+    float m_run[2] = {-INFINITY, -INFINITY};
+    float l_run[2] = {0.0f, 0.0f};
+    const float c = p.scale_log2;
+    const float th = kRescaleLog2 / c;
+    const h2 ones = h2{(half_t)1.0f, (half_t)1.0f};
+
+    const int nkb = (p.n_k + kKB - 1) / kKB;
+    if (head_ok) issue(0);
+    for (int kb = 0; kb < nkb; ++kb) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        // Slot (kb + 1) & 1 was last read in iteration kb - 1; every wave
+        // has passed the barrier above, so it is free.
+        if (HPW == 1 && kb + 1 < nkb) issue(kb + 1);
+        if (wave_active) {
+            const half_t* Ks = slot_ptr(kb);
+            const half_t* Vs = Ks + kKB * kD;
+            f16x s[2][2];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                s[k2][0] = f16x{};
+                s[k2][1] = f16x{};
+                const half_t* krow = Ks + (k2 * 32 + lrow) * kD;
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const h8 kf =
+                        *reinterpret_cast<const h8*>(krow + (((kk * 2 + lh) ^ kr_sw) << 3));
+                    s[k2][0] = mfma32x32x16(kf, qf[0][kk], s[k2][0]);
+                    s[k2][1] = mfma32x32x16(kf, qf[1][kk], s[k2][1]);
+                }
+            }
+            const int key_base = kb * kKB;
+            const bool tail = key_base + kKB > p.n_k;
+            h8 pf[2][4];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        float x = s[k2][qt][v];
+                        if (tail) {
+                            const int key = key_base + k2 * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                            if (key >= p.n_k) x = -INFINITY;
+                            s[k2][qt][v] = x;
+                        }
+                        mx = fmaxf(mx, x);
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                if (mx > m_run[qt] + th) {
+                    const float alpha = __builtin_amdgcn_exp2f((m_run[qt] - mx) * c);
+                    m_run[qt] = mx;
+                    l_run[qt] *= alpha;
+#pragma unroll
+                    for (int dm = 0; dm < 2; ++dm)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) o[qt][dm][v] *= alpha;
+                }
+                const float nmc = -m_run[qt] * c;
+                float ls = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int k2 = t >> 1, tp = t & 1;
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2) {
+                        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[k2][qt][8 * tp + e], c, nmc));
+                        const float p1 =
+                            __builtin_amdgcn_exp2f(fmaf(s[k2][qt][8 * tp + e + 1], c, nmc));
+                        const h2 pp = h2{(half_t)p0, (half_t)p1};
+                        pf[qt][t][e] = pp[0];
+                        pf[qt][t][e + 1] = pp[1];
+                        ls = __builtin_amdgcn_fdot2(pp, ones, ls, false);
+                    }
+                }
+                l_run[qt] += ls;
+            }
+            // O^T += V^T . P^T, four 16-key substeps.
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int dm = 0; dm < 2; ++dm) {
+                    const half_t* vp = Vs + t * 16 * kD + voff[dm];
+                    const h4 lo = lds_read_tr16(vp);
+                    const h4 hi = lds_read_tr16(vp + 8 * kD);
+                    const h8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                    o[0][dm] = mfma32x32x16(vf, pf[0][t], o[0][dm]);
+                    o[1][dm] = mfma32x32x16(vf, pf[1][t], o[1][dm]);
+                }
+            }
+        }
+        if (HPW == 4 && kb + 1 < nkb) {
+            // Single-block variant: reached only if a caller forced it onto a
+            // longer sequence; reload this wave's own slot after its reads.
+            __syncthreads();
+            if (head_ok) issue(kb + 1);
+        }
+    }
+
+    if (!wave_active) return;
+    half_t* ob = reinterpret_cast<half_t*>(p.out);
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int qi = q0 + qt * 32 + lrow;
+        const float l_tot = l_run[qt] + __shfl_xor(l_run[qt], 32, 64);
+        if (qi >= p.n_q) continue;
+        const int64_t tok = tok_q(p, seq, qi);
+        float scale = 1.0f / l_tot;
+        if (p.gates) scale *= p.gates[tok * p.H + h];
+        half_t* orow = ob + tok * p.ld_out + h * p.head_out;
+#pragma unroll
+        for (int dm = 0; dm < 2; ++dm)
+#pragma unroll
+            for (int gg = 0; gg < 4; ++gg) {
+                const int d = dm * 32 + 8 * gg + 4 * lh;
+                h4 val;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) val[e] = (half_t)(o[qt][dm][4 * gg + e] * scale);
+                *reinterpret_cast<h4*>(orow + d) = val;
+            }
+    }
+}
+
+// ===========================================================================
 // fp32
 // ===========================================================================
 template <int HPW>
@@ -537,6 +774,15 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnParams p) {
     }
 }
 
+// The DMA kernel addresses one (sequence, head) through a buffer descriptor
+// based at its first key: every key row must lie within 2^31 bytes of it,
+// and rows must be 16-byte aligned.
+bool dma_fits(const AttnParams& p) {
+    const int64_t rsb = p.k_pos * p.ld_in * 2;
+    if (p.k_pos < 0 || p.ld_in % 8 != 0 || p.head_in % 8 != 0) return false;
+    return (int64_t)(p.n_k - 1) * rsb + kD * 2 < ((int64_t)1 << 31);
+}
+
 int launch_attention(AttnParams& p, int64_t n_seq, int dtype, hipStream_t s) {
     const int hpw = p.n_q <= 64 && p.n_k <= 64 ? 4 : 1;
     const int wph = 4 / hpw;
@@ -546,6 +792,13 @@ int launch_attention(AttnParams& p, int64_t n_seq, int dtype, hipStream_t s) {
     p.per_xcd = (int)((p.total_items + 7) / 8);
     const int64_t grid = (int64_t)p.per_xcd * 8;
     if (grid > 0x7fffffff) return set_error(MSST_ERR_UNSUPPORTED, "attention grid too large");
+    if (dtype == MSST_F16 && p.cos_t == nullptr && dma_fits(p)) {
+        if (hpw == 4)
+            hipLaunchKernelGGL(attn_f16_dma_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL(attn_f16_dma_kernel<1>, dim3((unsigned)grid), dim3(256), 0, s, p);
+        return check_launch("attn_f16_dma_kernel");
+    }
     if (dtype == MSST_F16) {
         if (hpw == 4)
             hipLaunchKernelGGL(attn_f16_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, p);

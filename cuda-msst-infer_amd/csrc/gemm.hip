@@ -29,6 +29,8 @@
 // a row block (which share the same A rows) run together in one L2.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "msst_common.hpp"
 
 namespace msst {
@@ -83,22 +85,42 @@ constexpr int pick_ip() {
     return ip;
 }
 
+// Epilogue variants of store_tile_lds.
+constexpr int kEpiPlain = 0;  // act(acc + bias)
+constexpr int kEpiRes = 1;    // act(acc + bias) + residual
+constexpr int kEpiRope = 2;   // rotary embedding on the first `cols` columns
+
+// Interleaved-pair RoPE applied by the epilogue (ops_misc.cu:39-69 on the
+// q/k head columns): the output is rounded to fp16 first, as the reference
+// rotates the fp16 tensor the linear wrote, and rotated in fp32.  The
+// position of row r is (r / div) % mod; cos/sin are [positions, dh / 2].
+struct EpiRope {
+    const float* cos;
+    const float* sin;
+    int cols;  // columns [0, cols) are rotated (a multiple of dh)
+    int dh;    // head dim (pairs per position: dh / 2)
+    int div, mod;
+    float inv_div, inv_mod;
+};
+
 // Epilogue through LDS.  A wave's (MI*32) x (NI*32) accumulator block is
 // written to its LDS region IP fragment-rows at a time (static register
 // indices), then read back row-contiguously: each lane owns 4 consecutive
 // columns, so bias is loaded once and global stores are 16-byte (f32) /
 // 8-byte (f16) and row-contiguous.  The read-back runs in batches of U rows
-// per lane: residual loads of the batch first, then its LDS reads, then
-// math and stores — so stores never wait on each other (CDNA counts loads
-// and stores on one vmcnt; a global load inside a rolled loop would make
-// every iteration wait for all earlier stores).  RES is compile-time for
-// the same reason.  All waves run the same trip counts, so the block
-// barriers are uniform.  Caller: LDS free (after a barrier).
-template <int MI, int NI, int IP, bool RES, typename OutT>
+// per lane: the batch's global loads (residual rows, or RoPE cos/sin rows)
+// first, then its LDS reads, then math and stores — so stores never wait on
+// each other (CDNA counts loads and stores on one vmcnt; a global load
+// inside a rolled loop would make every iteration wait for all earlier
+// stores).  EPI is compile-time for the same reason.  All waves run the
+// same trip counts, so the block barriers are uniform.  Caller: LDS free
+// (after a barrier).
+template <int MI, int NI, int IP, int EPI, typename OutT>
 __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds, int lane,
                                                int row0, int col0, int M, int N,
                                                const float* __restrict__ bias, int act,
-                                               const OutT* residual, OutT* out, bool vec) {
+                                               const OutT* residual, OutT* out, bool vec,
+                                               const EpiRope& rope = EpiRope{}) {
     static_assert(MI % IP == 0, "IP must divide MI");
     constexpr int WN = NI * 32;
     constexpr int LPR = WN / 4;    // lanes per row
@@ -112,6 +134,10 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
     // Wave-uniform: the whole wave tile lies inside N with aligned rows, so
     // only one of the store paths below ever executes for a wave.
     const bool full = vec && col0 + WN <= N;
+    // Wave-uniform as well: rope.cols is a multiple of the 64-column wave
+    // tile whenever the host selects this epilogue.
+    const bool rope_on = EPI == kEpiRope && col0 + WN <= rope.cols;
+    const int pair = EPI == kEpiRope ? (col % rope.dh) >> 1 : 0;
     f4 bv = f4{0.0f, 0.0f, 0.0f, 0.0f};
     if (bias) {
 #pragma unroll
@@ -132,8 +158,8 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
         const int prow0 = row0 + p * IP * 32;
 #pragma unroll 1
         for (int it0 = 0; it0 < ITERS; it0 += U) {
-            f4 rv[U];
-            if constexpr (RES) {
+            f4 rv[U];  // residual values, or (cos, cos, sin, sin) of the 2 pairs
+            if constexpr (EPI == kEpiRes) {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int grow = prow0 + (it0 + u) * RPI + rr;
@@ -150,6 +176,21 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
                     }
                 }
             }
+            if constexpr (EPI == kEpiRope) {
+                if (rope_on) {
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const int grow = min(prow0 + (it0 + u) * RPI + rr, M - 1);
+                        int rem, pos;
+                        const int q = divmod24(grow, rope.div, rope.inv_div, rem);
+                        divmod24(q, rope.mod, rope.inv_mod, pos);
+                        const int t = pos * (rope.dh >> 1) + pair;
+                        const float2 c = *reinterpret_cast<const float2*>(rope.cos + t);
+                        const float2 sn = *reinterpret_cast<const float2*>(rope.sin + t);
+                        rv[u] = f4{c.x, c.y, sn.x, sn.y};
+                    }
+                }
+            }
             f4 v[U];
 #pragma unroll
             for (int u = 0; u < U; ++u)
@@ -161,7 +202,19 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
                     f4 o;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) o[e] = act_apply(v[u][e] + bv[e], act);
-                    if constexpr (RES) o += rv[u];
+                    if constexpr (EPI == kEpiRes) o += rv[u];
+                    if constexpr (EPI == kEpiRope) {
+                        if (rope_on) {
+#pragma unroll
+                            for (int e = 0; e < 2; ++e) {
+                                const float a = (float)(half_t)o[2 * e];
+                                const float b = (float)(half_t)o[2 * e + 1];
+                                const float c = rv[u][e], sn = rv[u][2 + e];
+                                o[2 * e] = a * c - b * sn;
+                                o[2 * e + 1] = a * sn + b * c;
+                            }
+                        }
+                    }
                     const int64_t idx = (int64_t)grow * N + col;
                     if (full) {
                         st4<OutT>(out + idx, o);
@@ -299,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(
     constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
     constexpr int kIP = pick_ip<MI, WN, kRegion>();
     static_assert(kIP * 32 * WN <= kRegion, "epilogue staging does not fit in LDS");
-    store_tile_lds<MI, NI, kIP, RES, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+    store_tile_lds<MI, NI, kIP, RES ? kEpiRes : kEpiPlain, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
                                       lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act, residual,
                                       out, vec != 0);
 }
@@ -425,7 +478,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
     constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
     constexpr int kIP = pick_ip<MI, WN, kRegion>();
     static_assert(kIP * 32 * WN <= kRegion, "epilogue staging does not fit in LDS");
-    store_tile_lds<MI, NI, kIP, RES, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+    store_tile_lds<MI, NI, kIP, RES ? kEpiRes : kEpiPlain, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
                                       lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act, residual,
                                       out, vec != 0);
 }
@@ -443,18 +496,6 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
 // are read from LDS while the MFMAs of kk run.  One vmcnt wait + barrier
 // per k-tile.
 // ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// 16-byte-per-lane DMA of buffer bytes [voffset, voffset + 16) into LDS at
-// lds + 16 * lane (lds is wave-uniform).  Offsets at or past `bytes` read
-// zero.  The buffer descriptor type only exists in device code, so kernels
-// reach it through this helper (a kernel naming it loses its host stub).
-__device__ __forceinline__ void dma16(const void* base, int bytes, half_t* lds, uint32_t voffset) {
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voffset, 0, 0, 0);
-}
-
 template <int BK>
 __device__ __forceinline__ int chunk_swz(int r) {
     // LDS rows of BK halves = BK/8 chunks of 16 B.  A b128 read is serviced
@@ -471,11 +512,11 @@ __device__ __forceinline__ int chunk_swz(int r) {
 // so a load has NSTG - 1 k-tiles of MFMA time to land.  MINB = workgroups
 // per CU the register/LDS budget is sized for (two for 256x128 tiles, so
 // one workgroup's epilogue overlaps the other's main loop).
-template <int BM, int BN, int BK, int NSTG, int MINB, bool RES, typename OutT>
+template <int BM, int BN, int BK, int NSTG, int MINB, int EPI, typename OutT>
 __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
     const half_t* __restrict__ A, const half_t* __restrict__ W, const float* __restrict__ bias,
     const OutT* residual, OutT* out, int M, int N, int K, int act, int tiles_n, int per_xcd,
-    int vec) {
+    int vec, EpiRope rope) {
     constexpr int CPR = BK / 8;              // 16-byte chunks per LDS row
     constexpr int RPD = 64 / CPR;            // rows per 1 KB DMA instruction
     constexpr int KK = BK / 16;              // MFMA k-substeps per k-tile
@@ -597,9 +638,9 @@ __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
     constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
     constexpr int kIP = pick_ip<MI, WN, kRegion>();
     static_assert(kIP * 32 * WN <= kRegion, "epilogue staging does not fit in LDS");
-    store_tile_lds<MI, NI, kIP, RES, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+    store_tile_lds<MI, NI, kIP, EPI, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
                                            lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act,
-                                           residual, out, vec != 0);
+                                           residual, out, vec != 0, rope);
 }
 
 // ---------------------------------------------------------------------------
@@ -900,19 +941,29 @@ int launch_f16(const void* x, bool x_f32, const half_t* w, const float* bias,
 
 template <int BM, int BN, int BK, int NSTG, int MINB, typename OutT>
 int launch_f16_dma(const half_t* x, const half_t* w, const float* bias, const OutT* res,
-                   OutT* out, int M, int N, int K, int act, hipStream_t s) {
+                   OutT* out, int M, int N, int K, int act, hipStream_t s,
+                   const EpiRope* rope = nullptr) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int per_xcd;
     int grid = num_xcd_slots((int64_t)tiles_m * tiles_n, per_xcd);
     const int vec = vec_flag(res, out, N);
-    if (res)
-        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, true, OutT>), dim3(grid),
-                           dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act, tiles_n,
-                           per_xcd, vec);
-    else
-        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, false, OutT>), dim3(grid),
-                           dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act, tiles_n,
-                           per_xcd, vec);
+    if (rope) {
+        if constexpr (std::is_same<OutT, half_t>::value) {
+            hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, kEpiRope, OutT>),
+                               dim3(grid), dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K,
+                               act, tiles_n, per_xcd, vec, *rope);
+        } else {
+            return set_error(MSST_ERR_UNSUPPORTED, "RoPE epilogue needs fp16 output");
+        }
+    } else if (res) {
+        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, kEpiRes, OutT>),
+                           dim3(grid), dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act,
+                           tiles_n, per_xcd, vec, EpiRope{});
+    } else {
+        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, kEpiPlain, OutT>),
+                           dim3(grid), dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act,
+                           tiles_n, per_xcd, vec, EpiRope{});
+    }
     return check_launch("gemm_f16_dma_kernel");
 }
 
@@ -1086,4 +1137,39 @@ extern "C" int msst_linear(const void* x, int x_dtype, const void* w, int w_dtyp
     if (out_dtype == MSST_F16)
         return dispatch<half_t>(x, x_dtype, w, w_dtype, bias, residual, out, M, K, N, act, s);
     return dispatch<float>(x, x_dtype, w, w_dtype, bias, residual, out, M, K, N, act, s);
+}
+
+extern "C" int msst_linear_rope(const void* x, const void* w, const float* bias, void* out,
+                                int64_t M, int64_t K, int64_t N, const float* cos_t,
+                                const float* sin_t, int64_t rope_cols, int64_t dim_head,
+                                int64_t pos_div, int64_t pos_mod, void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(x && w && out && cos_t && sin_t, MSST_ERR_INVALID_ARG, "null pointer");
+    MSST_REQUIRE(M >= 0 && K > 0 && N > 0, MSST_ERR_INVALID_ARG, "bad shape");
+    MSST_REQUIRE(dim_head > 0 && dim_head % 4 == 0 && rope_cols >= 0 && rope_cols <= N &&
+                     rope_cols % 64 == 0 && rope_cols % dim_head == 0,
+                 MSST_ERR_INVALID_ARG,
+                 "rope_cols must be a multiple of 64 and of dim_head (a multiple of 4), <= N");
+    MSST_REQUIRE(pos_div >= 1 && pos_mod >= 1 && pos_div < (1 << 24) && pos_mod < (1 << 24),
+                 MSST_ERR_INVALID_ARG, "bad position divisor / modulus");
+    MSST_REQUIRE(K % 64 == 0 && M < (1 << 24) && (M + 256) * K * 2 < ((int64_t)1 << 31) &&
+                     (N + 256) * K * 2 < ((int64_t)1 << 31),
+                 MSST_ERR_UNSUPPORTED, "shape outside the fused RoPE GEMM (K % 64, M < 2^24)");
+    MSST_REQUIRE(aligned(x, 16) && aligned(w, 16) && aligned(out, 16) && aligned(bias, 4) &&
+                     aligned(cos_t, 8) && aligned(sin_t, 8),
+                 MSST_ERR_ALIGNMENT, "x, w, out must be 16-byte and cos/sin 8-byte aligned");
+    if (M == 0) return MSST_OK;
+    EpiRope r{};
+    r.cos = cos_t;
+    r.sin = sin_t;
+    r.cols = (int)rope_cols;
+    r.dh = (int)dim_head;
+    r.div = (int)pos_div;
+    r.mod = (int)pos_mod;
+    r.inv_div = 1.0f / (float)pos_div;
+    r.inv_mod = 1.0f / (float)pos_mod;
+    return launch_f16_dma<256, 128, 32, 3, 2, half_t>(
+        reinterpret_cast<const half_t*>(x), reinterpret_cast<const half_t*>(w), bias, nullptr,
+        reinterpret_cast<half_t*>(out), (int)M, (int)N, (int)K, MSST_ACT_NONE, as_stream(stream),
+        &r);
 }

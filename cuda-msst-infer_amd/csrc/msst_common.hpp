@@ -60,6 +60,37 @@ __device__ __forceinline__ float to_f32(T v) { return (float)v; }
 template <typename T>
 __device__ __forceinline__ T from_f32(float v) { return (T)v; }
 
+// ---------------------------------------------------------------------------
+// LDS DMA (buffer_load_dwordx4 ... lds): lane l's 16 bytes at buffer offset
+// voffset land at lds + 16 * l (lds is wave-uniform).  Offsets at or past
+// `bytes` read zero.  The buffer descriptor type only exists in device code,
+// so kernels reach it through this helper (a kernel naming it loses its
+// host stub).
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void dma16(const void* base, int bytes, half_t* lds, uint32_t voffset) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voffset, 0, 0, 0);
+}
+
+// q = n / d, r = n % d for 0 <= n < 2^24, d >= 1, inv_d = 1.0f / d: the
+// float quotient is within one of the true one (relative error <= 2^-23,
+// n / d < 2^24 / d), and one correction step makes it exact.
+__device__ __forceinline__ int divmod24(int n, int d, float inv_d, int& r) {
+    int q = (int)((float)n * inv_d);
+    r = n - q * d;
+    if (r < 0) {
+        --q;
+        r += d;
+    } else if (r >= d) {
+        ++q;
+        r -= d;
+    }
+    return q;
+}
+
 // Butterfly sum over the 64 lanes of a wave.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -18,8 +18,8 @@
 //
 // Per transformer (fp16 weights):
 //   rms_norm_gate   x(f32) -> xn(f16), gates(f32)   [HBM]
-//   linear          xn -> qkv(f16)                   [MFMA]
-//   attention       qkv -> merged(f16) (RoPE, gate)  [MFMA]
+//   linear + RoPE   xn -> qkv(f16), q/k rotated      [MFMA]
+//   attention       qkv -> merged(f16) (gate)        [MFMA]
 //   linear + res    merged -> x += .                 [MFMA]
 //   rms_norm        x -> xn(f16)                     [HBM]
 //   linear + GELU   xn -> hidden(f16)                [MFMA]
@@ -78,6 +78,16 @@ bool desc_ok(const msst_stack_desc& d) {
         if (rc_ != MSST_OK) return rc_; \
     } while (0)
 
+// The fused QKV + RoPE GEMM covers fp16 weights with dim % 64 == 0,
+// 16-byte aligned w_qkv and fewer than 2^24 tokens.
+bool rope_in_gemm(const msst_stack_desc& d, const msst_layer_weights& w) {
+    const int64_t M = d.batch * d.frames * d.bands;
+    const int64_t hd = d.heads * d.dim_head;
+    return d.w_dtype == MSST_F16 && d.dim % 64 == 0 && (2 * hd) % 64 == 0 && M < (1 << 24) &&
+           (M + 256) * d.dim * 2 < ((int64_t)1 << 31) &&
+           (3 * hd + 256) * d.dim * 2 < ((int64_t)1 << 31) && aligned(w.w_qkv, 16);
+}
+
 int run_transformer(const msst_stack_desc& d, const msst_layer_weights& w, float* x, char* ws,
                     const StackBuffers& b, const msst_seq_layout& L, const float* cos_t,
                     const float* sin_t, hipStream_t s) {
@@ -94,10 +104,21 @@ int run_transformer(const msst_stack_desc& d, const msst_layer_weights& w, float
     // Attention block (model_bs_roformer.cu:242-283) + residual (:321-322).
     MSST_TRY(msst_rms_norm_gate(x, MSST_F32, w.attn_gamma, nscale, xn, dt, w.w_gate, dt, w.b_gate,
                                 gates, M, d.dim, (int)d.heads, s));
-    MSST_TRY(msst_linear(xn, dt, w.w_qkv, dt, nullptr, nullptr, qkv, dt, M, d.dim, 3 * hd,
-                         MSST_ACT_NONE, s));
-    MSST_TRY(msst_gated_rope_attention(qkv, dt, 3 * hd, cos_t, sin_t, gates, merged, hd, &L,
-                                       (int)d.heads, (int)d.dim_head, 0.0f, s));
+    if (rope_in_gemm(d, w)) {
+        // fp16: RoPE rides in the QKV GEMM epilogue (q and k columns); the
+        // attention kernel then reads pre-rotated q/k.  Position of token
+        // row r: (r / tok_pos) % seq_len for both axes of the time-major
+        // layout (time: t = r % T; frequency: f = (r / T) % F).
+        MSST_TRY(msst_linear_rope(xn, w.w_qkv, nullptr, qkv, M, d.dim, 3 * hd, cos_t, sin_t,
+                                  2 * hd, d.dim_head, L.tok_pos, L.seq_len, s));
+        MSST_TRY(msst_gated_rope_attention(qkv, dt, 3 * hd, nullptr, nullptr, gates, merged, hd,
+                                           &L, (int)d.heads, (int)d.dim_head, 0.0f, s));
+    } else {
+        MSST_TRY(msst_linear(xn, dt, w.w_qkv, dt, nullptr, nullptr, qkv, dt, M, d.dim, 3 * hd,
+                             MSST_ACT_NONE, s));
+        MSST_TRY(msst_gated_rope_attention(qkv, dt, 3 * hd, cos_t, sin_t, gates, merged, hd, &L,
+                                           (int)d.heads, (int)d.dim_head, 0.0f, s));
+    }
     MSST_TRY(msst_linear(merged, dt, w.w_out, dt, nullptr, x, x, MSST_F32, M, hd, d.dim,
                          MSST_ACT_NONE, s));
     // Feed-forward block (model_bs_roformer.cu:290-304) + residual (:325-326).

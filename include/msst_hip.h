@@ -17,6 +17,9 @@
  * Reference interfaces replaced (CUDA-MSST-Infer, src/):
  *   msst_linear                 ops.h:65-66, :128-135  (ops_linear.cu:150-427,
  *                               ops_fused.cu:203-303, :341-358)
+ *   msst_linear_rope            ops.h:66 + :99-100 fused (linear_no_bias of
+ *                               to_qkv, then apply_rotary_emb on q and k,
+ *                               model_bs_roformer.cu:249, :262)
  *   msst_rms_norm               ops.h:56               (ops_norm.cu:455-491)
  *   msst_rms_norm_gate          ops.h:56 + :134 fused  (rms_norm followed by
  *                               linear_sigmoid, model_bs_roformer.cu:243, :268)
@@ -76,6 +79,20 @@ const char* msst_last_error(void);
 int msst_linear(const void* x, int x_dtype, const void* w, int w_dtype,
                 const float* bias, const void* residual, void* out, int out_dtype,
                 int64_t M, int64_t K, int64_t N, int act, void* stream);
+
+/* fp16 out[M,N] = x[M,K] . w[N,K]^T (+ bias) with the interleaved-pair
+ * rotary embedding applied to columns [0, rope_cols): the value is rounded
+ * to fp16, then pair (2i, 2i+1) of each dim_head-wide head is rotated by
+ * (cos_t, sin_t)[pos, i] in fp32 and rounded again, pos = (row / pos_div) %
+ * pos_mod; tables are [pos_mod, dim_head / 2] fp32.  For a qkv projection
+ * rope_cols = 2 * H * dim_head (q and k heads; v passes through).  x, w, out
+ * f16.  Needs K % 64 == 0, rope_cols % 64 == 0, M < 2^24; otherwise
+ * MSST_ERR_UNSUPPORTED (use msst_linear + msst_gated_rope_attention with
+ * tables instead). */
+int msst_linear_rope(const void* x, const void* w, const float* bias, void* out,
+                     int64_t M, int64_t K, int64_t N, const float* cos_t,
+                     const float* sin_t, int64_t rope_cols, int64_t dim_head,
+                     int64_t pos_div, int64_t pos_mod, void* stream);
 
 /* y = x * rsqrt(sum(x^2) + 1e-12) * gamma * scale per row of D elements. */
 int msst_rms_norm(const void* x, int x_dtype, const float* gamma, float scale,

@@ -216,7 +216,11 @@ def _fused_reference(oracle, qkv, gates, cos_t, sin_t, B, F, T, H, axis):
 @pytest.mark.parametrize("B,F,T", [(1, 3, 70), (2, 5, 33), (1, 62, 801), (1, 60, 801)])
 @pytest.mark.parametrize("axis", ["time", "freq"])
 @pytest.mark.parametrize("dt", ["f32", "f16"])
-def test_gated_rope_attention(msst, oracle, cuda, B, F, T, axis, dt):
+@pytest.mark.parametrize("rope", ["tables", "prerotated"])
+def test_gated_rope_attention(msst, oracle, cuda, B, F, T, axis, dt, rope):
+    """rope="tables": RoPE applied inside the attention kernel;
+    rope="prerotated": no tables (q/k arrive rotated) — the fp16 LDS-DMA
+    kernel."""
     H, D = 8, 64
     rng = np.random.default_rng(B * 100 + F * 10 + T)
     M = B * F * T
@@ -225,14 +229,82 @@ def test_gated_rope_attention(msst, oracle, cuda, B, F, T, axis, dt):
         qkv = r16(qkv)
     gates = rng.uniform(0.0, 1.0, (M, H)).astype(np.float32)
     n = T if axis == "time" else F
-    c, s = oracle.rope_table(n, D)
+    c, s = oracle.rope_table(n, D) if rope == "tables" else (None, None)
     if axis == "time":
         L = msst.seq_layout(B * F, 1, T, T, 0, 1)
     else:
         L = msst.seq_layout(B, T, F, F * T, 1, T)
-    y = msst.gated_rope_attention(dev(qkv, tdt(dt)), L, H, dev(c), dev(s), dev(gates))
+    y = msst.gated_rope_attention(dev(qkv, tdt(dt)), L, H,
+                                  None if c is None else dev(c), None if s is None else dev(s),
+                                  dev(gates))
     r = _fused_reference(oracle, qkv, gates, c, s, B, F, T, H, axis)
     assert rel_err(host(y), r) < tol(dt)
+
+
+@pytest.mark.parametrize("N,growth", [(801, 0.02), (300, 0.2), (130, 3.0)])
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_attention_rising_scores(msst, oracle, cuda, N, growth, dt):
+    """Scores that grow along the key axis: the running max rises in every
+    key block (the fp16 kernel's deferred rescale fires repeatedly), up to
+    score spreads of hundreds where most probabilities underflow."""
+    rng = np.random.default_rng(N)
+    q = rng.standard_normal((1, 2, N, 64)).astype(np.float32)
+    k = rng.standard_normal((1, 2, N, 64)).astype(np.float32) * 0.5
+    # push key n along its query's direction so q.k_n grows with n
+    qm = q.mean(axis=2, keepdims=True)
+    k = k + growth * np.arange(N, dtype=np.float32)[None, None, :, None] * qm / 8
+    v = rng.standard_normal((1, 2, N, 64)).astype(np.float32)
+    if dt == "f16":
+        q, k, v = r16(q), r16(k), r16(v)
+    y = msst.attention(dev(q, tdt(dt)), dev(k, tdt(dt)), dev(v, tdt(dt)))
+    r = oracle.attention(q, k, v)
+    assert np.isfinite(host(y)).all()
+    assert rel_err(host(y), r) < tol(dt)
+
+
+# ------------------------------------------------------- fused QKV + RoPE
+def _rope_rows(oracle, y, c, s, B, F, T, H, axis, rope_cols):
+    """Apply the oracle RoPE to columns [0, rope_cols) of token rows y in
+    [B,F,T] order, position t (time) or f (freq)."""
+    D = 64
+    n_heads = rope_cols // D
+    out = y.copy()
+    part = y[:, :rope_cols].reshape(B, F, T, n_heads, D)
+    if axis == "time":
+        seqs = part.reshape(B * F, T, n_heads, D).transpose(0, 2, 1, 3)
+    else:
+        seqs = part.transpose(0, 2, 3, 1, 4).reshape(B * T, n_heads, F, D)
+    rot, _ = oracle.rope_apply(np.ascontiguousarray(seqs), np.ascontiguousarray(seqs), c, s)
+    if axis == "time":
+        back = rot.transpose(0, 2, 1, 3).reshape(B * F * T, rope_cols)
+    else:
+        back = rot.reshape(B, T, n_heads, F, D).transpose(0, 3, 1, 2, 4).reshape(B * F * T,
+                                                                                 rope_cols)
+    out[:, :rope_cols] = back
+    return out
+
+
+@pytest.mark.parametrize("B,F,T", [(1, 3, 70), (2, 5, 33), (1, 62, 801)])
+@pytest.mark.parametrize("axis", ["time", "freq"])
+@pytest.mark.parametrize("K,H", [(512, 8), (384, 8), (128, 2)])
+def test_linear_rope(msst, oracle, cuda, B, F, T, axis, K, H):
+    """fp16 x . W^T, rounded to fp16, q/k head columns rotated at each
+    token's position — against the oracle linear followed by the oracle
+    RoPE on the fp16-rounded product."""
+    D = 64
+    M = B * F * T
+    N = 3 * H * D
+    rng = np.random.default_rng(M + K + H)
+    x = r16(rng.standard_normal((M, K)).astype(np.float32))
+    w = r16((rng.standard_normal((N, K)) * 0.05).astype(np.float32))
+    n = T if axis == "time" else F
+    c, s = oracle.rope_table(n, D)
+    div = 1 if axis == "time" else T
+    y = msst.linear_rope(dev(x, torch.float16), dev(w, torch.float16), dev(c), dev(s),
+                         2 * H * D, D, div, n)
+    lin = r16(oracle.linear(x, w))
+    r = _rope_rows(oracle, lin, c, s, B, F, T, H, axis, 2 * H * D)
+    assert rel_err(host(y), r) < 2e-3
 
 
 # ----------------------------------------------------------------- layout
