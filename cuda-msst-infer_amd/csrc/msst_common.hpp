@@ -44,11 +44,32 @@ __device__ __forceinline__ f16x mfma32x32x2f32(float a, float b, f16x c) {
 }
 
 // ---------------------------------------------------------------------------
-// Epilogue activations.  erff/expf are the ROCm device-library routines
-// (not fast-math approximations): the fp32 path is held to 1e-4.
+// Epilogue activations.
+// GELU(v) = v/2 (1 + erf(v / sqrt 2)) with erf from Abramowitz & Stegun,
+// Handbook of Mathematical Functions (1964), formula 7.1.26:
+//   erf(z) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),
+//   t = 1 / (1 + p z), z >= 0,  |error| <= 1.5e-7,
+// odd extension for z < 0.  Sixteen VALU operations (v_rcp_f32 and
+// v_exp_f32 among them) against several times that for the library erff,
+// which dominated the FF1 epilogue; 1.5e-7 absolute is far below the fp16
+// output rounding and the 1e-4 fp32 tolerance.
+// sigmoid / SiLU use the ROCm device-library expf.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ float erf_as7126(float z) {
+    const float a = fabsf(z);
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, a, 1.0f));
+    float poly = fmaf(t, 1.061405429f, -1.453152027f);
+    poly = fmaf(t, poly, 1.421413741f);
+    poly = fmaf(t, poly, -0.284496736f);
+    poly = fmaf(t, poly, 0.254829592f);
+    poly *= t;
+    // exp(-a^2) = 2^(-a^2 log2 e); v_exp_f32 flushes to 0 far out.
+    const float e = __builtin_amdgcn_exp2f(-(a * a) * 1.4426950408889634f);
+    return copysignf(fmaf(-poly, e, 1.0f), z);
+}
+
 __device__ __forceinline__ float act_apply(float v, int act) {
-    if (act == MSST_ACT_GELU) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    if (act == MSST_ACT_GELU) return 0.5f * v * (1.0f + erf_as7126(v * 0.70710678118654752f));
     if (act == MSST_ACT_SIGMOID) return 1.0f / (1.0f + expf(-v));
     if (act == MSST_ACT_SILU) return v / (1.0f + expf(-v));
     return v;

@@ -13,6 +13,8 @@
 // a reduce-scatter butterfly: the first shuffle halves the set of values a
 // lane carries, so 8 gates cost 10 shuffles instead of 8 x 6.  Other D take
 // a two-pass scalar path.  HBM-bound: bytes per row = D*(in + out) + 4G.
+#include <type_traits>
+
 #include "msst_common.hpp"
 
 namespace msst {
@@ -131,6 +133,97 @@ __global__ __launch_bounds__(kThreads) void rms_norm_vec_kernel(
     }
 }
 
+// fp16 output and fp16 gate weights (the Roformer fp16 path): each wave
+// walks a grid-stride run of rows and keeps its slice of gamma and of
+// W_gate [G, D] in registers for the whole run (NS slots of 4 columns per
+// lane, D <= 256 * NS), so W_gate is read once per wave instead of once per
+// row.  The gate dot products run on the fp16-rounded y with v_dot2_f32_f16
+// (fp32 accumulation of exact fp16 products, as a GEMM over the stored y
+// computes them).  The next row's x is loaded before the current row is
+// processed.
+template <typename XT, int NS, int GP>
+__global__ __launch_bounds__(kThreads) void rms_norm_gate_h_kernel(
+    const XT* __restrict__ x, const float* __restrict__ gamma, float scale,
+    half_t* __restrict__ out, const half_t* __restrict__ wg, const float* __restrict__ bg,
+    float* __restrict__ gates, int64_t rows, int D, int G) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave0 = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int64_t nwaves = (int64_t)gridDim.x * kRowsPerBlock;
+    if (wave0 >= rows) return;
+    f4 gm[NS];
+    h2 wr[NS][GP][2];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+        const int j = 4 * (64 * i + lane);
+        const bool in = j < D;
+        gm[i] = in ? *reinterpret_cast<const f4*>(gamma + j) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < GP; ++g) {
+            h4 w = h4{};
+            if (in && g < G) w = *reinterpret_cast<const h4*>(wg + (int64_t)g * D + j);
+            wr[i][g][0] = h2{w[0], w[1]};
+            wr[i][g][1] = h2{w[2], w[3]};
+        }
+    }
+    f4 v[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+        const int j = 4 * (64 * i + lane);
+        v[i] = j < D ? load4<XT>(x + wave0 * D + j) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    for (int64_t row = wave0; row < rows; row += nwaves) {
+        const int64_t nxt = row + nwaves;
+        f4 vn[NS];
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            const int j = 4 * (64 * i + lane);
+            vn[i] = (nxt < rows && j < D) ? load4<XT>(x + nxt * D + j)
+                                          : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NS; ++i)
+            ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss + 1e-12f);
+        float gacc[GP];
+#pragma unroll
+        for (int g = 0; g < GP; ++g) gacc[g] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            const int j = 4 * (64 * i + lane);
+            h4 y;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = (half_t)(v[i][e] * inv * gm[i][e] * scale);
+            if (j < D) *reinterpret_cast<h4*>(out + row * D + j) = y;
+            const h2 y0 = h2{y[0], y[1]}, y1 = h2{y[2], y[3]};
+#pragma unroll
+            for (int g = 0; g < GP; ++g) {
+                gacc[g] = __builtin_amdgcn_fdot2(y0, wr[i][g][0], gacc[g], false);
+                gacc[g] = __builtin_amdgcn_fdot2(y1, wr[i][g][1], gacc[g], false);
+            }
+        }
+        float sg = reduce_scatter<GP>(gacc, lane);
+        constexpr int SHIFT = GP == 16 ? 2 : 3;
+        const int g = lane >> SHIFT;
+        if ((lane & ((1 << SHIFT) - 1)) == 0 && g < G)
+            gates[row * G + g] = 1.0f / (1.0f + expf(-(sg + bg[g])));
+#pragma unroll
+        for (int i = 0; i < NS; ++i) v[i] = vn[i];
+    }
+}
+
+template <typename XT, int NS, int GP>
+void launch_gate_h(const void* x, const float* gamma, float scale, void* out, const void* wg,
+                   const float* bg, float* gates, int64_t rows, int D, int G, hipStream_t s) {
+    int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    if (blocks > 1024) blocks = 1024;
+    hipLaunchKernelGGL((rms_norm_gate_h_kernel<XT, NS, GP>), dim3((unsigned)blocks),
+                       dim3(kThreads), 0, s, reinterpret_cast<const XT*>(x), gamma, scale,
+                       reinterpret_cast<half_t*>(out), reinterpret_cast<const half_t*>(wg), bg,
+                       gates, rows, D, G);
+}
+
 // Any D: two passes over the row, scalar accesses.
 template <typename XT, typename OutT, typename WT, int GP>
 __global__ __launch_bounds__(kThreads) void rms_norm_scalar_kernel(
@@ -199,6 +292,27 @@ int dispatch_gate(const void* x, const float* gamma, float scale, void* out, con
     if (G == 0)
         return launch_norm<XT, OutT, float, 0>(x, gamma, scale, out, nullptr, nullptr, nullptr,
                                                rows, D, 0, s);
+    if constexpr (std::is_same<OutT, half_t>::value) {
+        // Register-resident W_gate path: D % 4 == 0, D <= 1024, aligned rows.
+        const bool fast = w_dtype == MSST_F16 && D % 4 == 0 && D <= 1024 &&
+                          aligned(x, 4 * sizeof(XT)) && aligned(out, 8) && aligned(gamma, 16) &&
+                          aligned(wg, 8);
+        if (fast) {
+            const int ns = (D + 255) / 256;
+            if (G <= 8) {
+                if (ns == 1) launch_gate_h<XT, 1, 8>(x, gamma, scale, out, wg, bg, gates, rows, D, G, s);
+                else if (ns == 2) launch_gate_h<XT, 2, 8>(x, gamma, scale, out, wg, bg, gates, rows, D, G, s);
+                else if (ns == 3) launch_gate_h<XT, 3, 8>(x, gamma, scale, out, wg, bg, gates, rows, D, G, s);
+                else launch_gate_h<XT, 4, 8>(x, gamma, scale, out, wg, bg, gates, rows, D, G, s);
+            } else {
+                if (ns == 1) launch_gate_h<XT, 1, 16>(x, gamma, scale, out, wg, bg, gates, rows, D, G, s);
+                else if (ns == 2) launch_gate_h<XT, 2, 16>(x, gamma, scale, out, wg, bg, gates, rows, D, G, s);
+                else if (ns == 3) launch_gate_h<XT, 3, 16>(x, gamma, scale, out, wg, bg, gates, rows, D, G, s);
+                else launch_gate_h<XT, 4, 16>(x, gamma, scale, out, wg, bg, gates, rows, D, G, s);
+            }
+            return check_launch("rms_norm_gate_h_kernel");
+        }
+    }
     if (w_dtype == MSST_F16) {
         if (G <= 8)
             return launch_norm<XT, OutT, half_t, 8>(x, gamma, scale, out, wg, bg, gates, rows, D,

@@ -102,6 +102,33 @@ def test_linear_small(msst, oracle, cuda, M, K, N, wd, xd, od, act):
 
 
 @pytest.mark.parametrize("wd", ["f16", "f32"])
+def test_gelu_error_bound(msst, cuda, wd):
+    """The epilogue GELU (Abramowitz & Stegun 7.1.26 erf, |error| <= 1.5e-7)
+    against float64 erf.  W = I makes the pre-activation exactly x, so the
+    measured error is the activation's own: <= 5e-7 |x| (approximation plus
+    fp32 evaluation) for fp32 output, plus half an fp16 ulp for fp16 output."""
+    from scipy.special import erf
+    n = 64
+    x = np.linspace(-12.0, 12.0, 4096 * n, dtype=np.float64)
+    x = np.concatenate([x, [0.0, 1e-30, -1e-30, 5e-8, -5e-8] + [0.0] * (n - 5)])
+    x = x.astype(np.float32)
+    if wd == "f16":
+        x = r16(x)
+    x = x.reshape(-1, n)
+    w = np.eye(n, dtype=np.float32)
+    exact = 0.5 * x.astype(np.float64) * (1.0 + erf(x.astype(np.float64) / np.sqrt(2.0)))
+    y32 = host(msst.linear(dev(x, tdt(wd)), dev(w, tdt(wd)), None, "gelu",
+                           out_dtype=torch.float32)).astype(np.float64)
+    bound = 5e-7 * np.abs(x) + 1e-30
+    assert np.all(np.abs(y32 - exact) <= bound), float(np.max(np.abs(y32 - exact) / bound))
+    y16 = host(msst.linear(dev(x, tdt(wd)), dev(w, tdt(wd)), None, "gelu",
+                           out_dtype=torch.float16)).astype(np.float64)
+    half_ulp = np.abs(exact).astype(np.float16).astype(np.float64)
+    half_ulp = np.maximum(np.spacing(half_ulp.astype(np.float16)).astype(np.float64) / 2, 2.0**-25)
+    assert np.all(np.abs(y16 - exact) <= bound + half_ulp)
+
+
+@pytest.mark.parametrize("wd", ["f16", "f32"])
 def test_linear_residual_in_place(msst, oracle, cuda, wd):
     rng = np.random.default_rng(5)
     M, K, N = 777, 512, 384
