@@ -1,0 +1,218 @@
+// ops.cpp — cudasep::ops on the MI355X C ABI.  See ops.h for the dtype
+// rules; each function cites the reference function it stands in for.
+#include "ops.h"
+
+#include <cmath>
+#include <string>
+
+#include "memory_pool.h"
+#include "msst_hip.h"
+
+namespace cudasep {
+
+bool g_quantize_fp16 = false;
+bool g_enable_cuda_graph_attention = true;
+
+void clear_attention_graph_cache() {}
+
+CudaContext& CudaContext::instance() {
+    static CudaContext ctx;
+    return ctx;
+}
+
+void CudaContext::sync() { HIP_CHECK(hipDeviceSynchronize()); }
+
+namespace ops {
+namespace {
+
+int abi(DType dt) {
+    if (dt == DType::Float32) return MSST_F32;
+    if (dt == DType::Float16) return MSST_F16;
+    throw std::runtime_error("cudasep::ops: int64 tensors are not supported here");
+}
+
+void check(int rc, const char* what) {
+    if (rc != MSST_OK) throw std::runtime_error(std::string(what) + ": " + msst_last_error());
+}
+
+void* stream() { return CudaContext::instance().stream(); }
+
+// Biases, gammas and RoPE tables are consumed as fp32 (the reference's
+// ensure_f32 on them).
+Tensor f32(const Tensor& t) { return t.to_f32(); }
+
+std::vector<int64_t> with_last(const std::vector<int64_t>& s, int64_t last) {
+    std::vector<int64_t> o = s;
+    o.back() = last;
+    return o;
+}
+
+// Shared GEMM driver: act(x . W^T + b) written as out_dtype.
+Tensor gemm(const char* name, const Tensor& x, const Tensor& w, const Tensor* bias, int act,
+            DType out_dtype) {
+    if (w.ndim() != 2) throw std::runtime_error(std::string(name) + ": weight must be 2-D [out, in]");
+    if (x.ndim() < 1) throw std::runtime_error(std::string(name) + ": x must have a last dim");
+    const int64_t N = w.size(0), K = w.size(1);
+    if (x.size(-1) != K)
+        throw std::runtime_error(std::string(name) + ": x " + x.shape_str() + " does not match W " +
+                                 w.shape_str());
+    Tensor b;
+    if (bias) {
+        if (bias->numel() != N)
+            throw std::runtime_error(std::string(name) + ": bias has " +
+                                     std::to_string(bias->numel()) + " elements, W has " +
+                                     std::to_string(N) + " rows");
+        b = f32(*bias);
+    }
+    const int64_t M = K > 0 ? x.numel() / K : 0;
+    Tensor out = Tensor::empty(with_last(x.shape(), N), out_dtype);
+    if (M > 0)
+        check(msst_linear(x.data_ptr(), abi(x.dtype()), w.data_ptr(), abi(w.dtype()),
+                          bias ? b.data_f32() : nullptr, nullptr, out.data_ptr(), abi(out_dtype),
+                          M, K, N, act, stream()),
+              name);
+    return out;
+}
+
+// linear / linear_no_bias: fp16 W -> fp32 out; fp32 W -> x's dtype.
+DType plain_out(const Tensor& x, const Tensor& w) {
+    return w.dtype() == DType::Float16 ? DType::Float32 : x.dtype();
+}
+// Fused activations: fp16 when x is fp16, else fp32.
+DType act_out(const Tensor& x) { return x.dtype() == DType::Float16 ? DType::Float16 : DType::Float32; }
+
+}  // namespace
+
+// ops_norm.cu:455-491
+Tensor rms_norm(const Tensor& x, const Tensor& gamma, float scale) {
+    if (x.ndim() < 1) throw std::runtime_error("rms_norm: x must have a last dim");
+    const int64_t D = x.size(-1);
+    if (gamma.numel() != D)
+        throw std::runtime_error("rms_norm: gamma has " + std::to_string(gamma.numel()) +
+                                 " elements, rows have " + std::to_string(D));
+    Tensor g = f32(gamma);
+    Tensor out = Tensor::empty(x.shape(), x.dtype());
+    const int64_t rows = D > 0 ? x.numel() / D : 0;
+    if (rows > 0)
+        check(msst_rms_norm(x.data_ptr(), abi(x.dtype()), g.data_f32(), scale, out.data_ptr(),
+                            abi(x.dtype()), rows, D, stream()),
+              "rms_norm");
+    return out;
+}
+
+// ops_linear.cu:150-343
+Tensor linear(const Tensor& x, const Tensor& weight, const Tensor& bias) {
+    return gemm("linear", x, weight, &bias, MSST_ACT_NONE, plain_out(x, weight));
+}
+
+// ops_linear.cu:349-427
+Tensor linear_no_bias(const Tensor& x, const Tensor& weight) {
+    return gemm("linear_no_bias", x, weight, nullptr, MSST_ACT_NONE, plain_out(x, weight));
+}
+
+// ops_fused.cu:264-282
+Tensor linear_gelu(const Tensor& x, const Tensor& weight, const Tensor& bias) {
+    return gemm("linear_gelu", x, weight, &bias, MSST_ACT_GELU, act_out(x));
+}
+
+// ops_fused.cu:341-358
+Tensor linear_silu(const Tensor& x, const Tensor& weight, const Tensor& bias) {
+    return gemm("linear_silu", x, weight, &bias, MSST_ACT_SILU, act_out(x));
+}
+
+// ops_fused.cu:285-303
+Tensor linear_sigmoid(const Tensor& x, const Tensor& weight, const Tensor& bias) {
+    return gemm("linear_sigmoid", x, weight, &bias, MSST_ACT_SIGMOID, act_out(x));
+}
+
+// ops_attention.cu:522-599 (fused flash attention instead of the
+// materialised QK^T / softmax / PV pipeline).
+Tensor scaled_dot_product_attention(const Tensor& q, const Tensor& k, const Tensor& v,
+                                    float scale, float /*dropout*/) {
+    if (q.ndim() != 4 || k.ndim() != 4 || v.ndim() != 4)
+        throw std::runtime_error("scaled_dot_product_attention: q, k, v must be 4-D [B,H,N,D]");
+    const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3), Nk = k.size(2);
+    if (k.size(0) != B || k.size(1) != H || k.size(3) != D || v.size(0) != B ||
+        v.size(1) != H || v.size(2) != Nk || v.size(3) != D)
+        throw std::runtime_error("scaled_dot_product_attention: shapes q " + q.shape_str() +
+                                 ", k " + k.shape_str() + ", v " + v.shape_str() +
+                                 " do not agree");
+    // One element type for the kernel: k and v follow q.
+    Tensor kc = k.to_dtype(q.dtype()), vc = v.to_dtype(q.dtype());
+    Tensor out = Tensor::empty(q.shape(), q.dtype());
+    check(msst_attention(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
+                         abi(q.dtype()), B, H, N, Nk, D, scale, stream()),
+          "scaled_dot_product_attention");
+    return out;
+}
+
+// ops_misc.cu:73-131 (in place; the fp16 path rotates in fp32 registers and
+// writes fp16 back, without the reference's f32 round trip tensors).
+void apply_rotary_emb(Tensor& q, Tensor& k, const Tensor& cos_freqs, const Tensor& sin_freqs) {
+    if (q.ndim() != 4 || k.ndim() != 4)
+        throw std::runtime_error("apply_rotary_emb: q and k must be 4-D [B,H,N,D]");
+    if (q.shape() != k.shape() || q.dtype() != k.dtype())
+        throw std::runtime_error("apply_rotary_emb: q and k must share shape and dtype");
+    const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
+    if (cos_freqs.numel() < N * (D / 2) || sin_freqs.numel() < N * (D / 2))
+        throw std::runtime_error("apply_rotary_emb: cos/sin tables smaller than [N, D/2]");
+    Tensor c = f32(cos_freqs), s = f32(sin_freqs);
+    check(msst_rope_qk(q.data_ptr(), k.data_ptr(), abi(q.dtype()), c.data_f32(), s.data_f32(), B,
+                       H, N, D, stream()),
+          "apply_rotary_emb");
+}
+
+// model_bs_roformer.cu:482-539 / model_mel_band_roformer.cu:843-906
+void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int heads, int dim_head,
+                    const Tensor& final_gamma) {
+    if (x.ndim() != 4 || x.dtype() != DType::Float32)
+        throw std::runtime_error("roformer_stack: x must be fp32 [B, T, F, dim]");
+    if (layers.size() % 2 != 0)
+        throw std::runtime_error("roformer_stack: layers must alternate time/frequency (even count)");
+    msst_stack_desc d{};
+    d.batch = x.size(0);
+    d.frames = x.size(1);
+    d.bands = x.size(2);
+    d.dim = x.size(3);
+    d.heads = heads;
+    d.dim_head = dim_head;
+    d.depth = (int64_t)layers.size() / 2;
+    d.ff_dim = layers.empty() ? 4 * d.dim : layers[0].w_ff1.size(0);
+    const DType wdt = layers.empty() ? DType::Float32 : layers[0].w_qkv.dtype();
+    d.w_dtype = abi(wdt);
+    // fp32 copies of the vectors, kept alive for the call.
+    std::vector<Tensor> keep;
+    std::vector<msst_layer_weights> lw(layers.size());
+    auto vec = [&](const Tensor& t) -> const float* {
+        if (t.is_empty()) return nullptr;
+        keep.push_back(f32(t));
+        return keep.back().data_f32();
+    };
+    keep.reserve(layers.size() * 8 + 1);
+    for (size_t i = 0; i < layers.size(); ++i) {
+        const RoformerLayer& L = layers[i];
+        for (const Tensor* m : {&L.w_qkv, &L.w_gate, &L.w_out, &L.w_ff1, &L.w_ff2})
+            if (m->dtype() != wdt)
+                throw std::runtime_error("roformer_stack: weight matrices must share one dtype");
+        lw[i].attn_gamma = vec(L.attn_gamma);
+        lw[i].w_qkv = L.w_qkv.data_ptr();
+        lw[i].w_gate = L.w_gate.data_ptr();
+        lw[i].b_gate = vec(L.b_gate);
+        lw[i].w_out = L.w_out.data_ptr();
+        lw[i].ff_gamma = vec(L.ff_gamma);
+        lw[i].w_ff1 = L.w_ff1.data_ptr();
+        lw[i].b_ff1 = vec(L.b_ff1);
+        lw[i].w_ff2 = L.w_ff2.data_ptr();
+        lw[i].b_ff2 = vec(L.b_ff2);
+        lw[i].final_gamma = vec(L.final_gamma);
+    }
+    const float* fg = vec(final_gamma);
+    const int64_t ws = msst_roformer_stack_workspace(&d);
+    if (ws < 0) throw std::runtime_error(std::string("roformer_stack: ") + msst_last_error());
+    Tensor work = Tensor::empty({ws}, DType::Float16);  // byte buffer (>= ws bytes)
+    check(msst_roformer_stack(x.data_f32(), &d, lw.data(), fg, work.data_ptr(), 2 * ws, stream()),
+          "roformer_stack");
+}
+
+}  // namespace ops
+}  // namespace cudasep

@@ -1,0 +1,52 @@
+"""The C++ drop-in surface (cudasep::Tensor / cudasep::ops, libcudasep_amd.so).
+
+CPU: the library exports the reference's op names with the reference's
+signatures (src/ops.h:56, :65-66, :83-85, :99-100, :128-135).
+GPU: tests/cpp/test_host_ops checks every op against the CPU oracle, the
+dtype rules and the error behaviour (see that file for the tolerances).
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HOST_LIB = os.path.join(ROOT, "cuda-msst-infer_amd", "libcudasep_amd.so")
+TEST_BIN = os.path.join(ROOT, "tests", "cpp", "_build", "test_host_ops")
+
+SIGNATURES = [
+    "cudasep::ops::linear(cudasep::Tensor const&, cudasep::Tensor const&, cudasep::Tensor const&)",
+    "cudasep::ops::linear_no_bias(cudasep::Tensor const&, cudasep::Tensor const&)",
+    "cudasep::ops::linear_gelu(cudasep::Tensor const&, cudasep::Tensor const&, cudasep::Tensor const&)",
+    "cudasep::ops::linear_silu(cudasep::Tensor const&, cudasep::Tensor const&, cudasep::Tensor const&)",
+    "cudasep::ops::linear_sigmoid(cudasep::Tensor const&, cudasep::Tensor const&, cudasep::Tensor const&)",
+    "cudasep::ops::rms_norm(cudasep::Tensor const&, cudasep::Tensor const&, float)",
+    "cudasep::ops::apply_rotary_emb(cudasep::Tensor&, cudasep::Tensor&, cudasep::Tensor const&, cudasep::Tensor const&)",
+    "cudasep::ops::scaled_dot_product_attention(cudasep::Tensor const&, cudasep::Tensor const&, cudasep::Tensor const&, float, float)",
+    "cudasep::clear_attention_graph_cache()",
+    "cudasep::CudaContext::instance()",
+    "cudasep::Tensor::empty(std::vector<long, std::allocator<long> >, cudasep::DType)",
+]
+
+
+def test_host_library_exports_reference_signatures():
+    assert os.path.exists(HOST_LIB), "build libcudasep_amd.so first (make -C cuda-msst-infer_amd)"
+    out = subprocess.run(["nm", "-DC", "--defined-only", HOST_LIB], check=True,
+                         capture_output=True, text=True).stdout
+    for sig in SIGNATURES:
+        assert sig in out, sig
+    for glob in ("cudasep::g_quantize_fp16", "cudasep::g_enable_cuda_graph_attention"):
+        assert glob in out, glob
+
+
+@pytest.mark.gpu
+def test_host_ops_against_oracle(cuda):
+    assert os.path.exists(TEST_BIN), "build tests/cpp first (make -C tests/cpp)"
+    print("running", TEST_BIN, flush=True)
+    r = subprocess.run([TEST_BIN], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-4000:])
+    print(r.stderr[-2000:])
+    assert r.returncode == 0
+    assert r.stdout.rstrip().splitlines()[-1].startswith("OK:")
