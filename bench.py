@@ -13,12 +13,19 @@ Prints ONE JSON line:
   value          ms per 8 s chunk (lower is better), inputs resident in HBM
   gemm_tflops    the stack's MFMA GEMMs replayed alone (same shapes, same
                  epilogues, same stream) -> TFLOP/s and fraction of peak
-  roofline       dominant kernel = gemm_f16_kernel on the FF1 shape
+  roofline       dominant kernel = gemm_f16_dma_kernel on the FF1 shape
                  (M=49662, K=512, N=2048, bias+GELU, fp16 out), HIP-event
-                 timed over the launches of its own timed loop
-  cpu_baseline   the fp32 CPU oracle on a bounded sample (one depth of the
-                 stack = 1/12 of the chunk), extrapolated to ms per chunk
-  parity         GPU vs oracle on that same one-depth sample
+                 timed over 50 launches on the stream it runs on; traffic =
+                 HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE
+                 (profiles/gemm_ff1_traffic.json), copy-kernel calibrated
+  kernels        every kernel of one transformer, timed alone (us/launch),
+                 with TFLOP/s (MFMA-bound) or GB/s (HBM-bound)
+  cpu_baseline   the fp32 CPU oracle on one whole chunk (about 10 s of CPU
+                 work on 16 threads)
+  parity         GPU vs oracle on that same chunk (same weights and input)
+  pcie_inclusive_ms_per_chunk
+                 the same step with the chunk handed over in pinned host
+                 memory (H2D copy + stack + D2H copy); never `value`
 """
 from __future__ import annotations
 
@@ -106,10 +113,16 @@ def gemm_replay(msst, torch, layers, batch):
     merged = torch.randn(M, hd, device="cuda").half()
     hidden = torch.empty(M, FF, device="cuda", dtype=torch.float16)
     res = torch.randn(M, DIM, device="cuda")
+    tcos, tsin = msst.rope_table_device(FRAMES, DH)
+    fcos, fsin = msst.rope_table_device(BANDS, DH)
 
     def run():
-        for w in layers:
-            msst.linear(xn, w["w_qkv"], out=qkv)
+        for i, w in enumerate(layers):
+            # QKV with the RoPE epilogue, time / frequency positions as in the stack.
+            if i % 2 == 0:
+                msst.linear_rope(xn, w["w_qkv"], tcos, tsin, 2 * hd, DH, 1, FRAMES, out=qkv)
+            else:
+                msst.linear_rope(xn, w["w_qkv"], fcos, fsin, 2 * hd, DH, FRAMES, BANDS, out=qkv)
             msst.linear(merged, w["w_out"], residual=res, out=res)
             msst.linear(xn, w["w_ff1"], w["b_ff1"], "gelu", out=hidden)
             msst.linear(hidden, w["w_ff2"], w["b_ff2"], residual=res, out=res)
@@ -117,8 +130,10 @@ def gemm_replay(msst, torch, layers, batch):
 
 
 def cpu_baseline_and_parity(msst, torch, args):
-    """Oracle on one depth (time + frequency transformer) of the stack at
-    full size; the GPU runs the same depth for the parity figure."""
+    """Oracle on the whole workload (one 8 s chunk through the 12-depth
+    stack, BSRoformer final norm) with its own seeded weights — about 10 s of
+    CPU work on 16 host threads; the GPU runs the same stack on the same
+    weights and input for the parity figure."""
     import numpy as np
     sys.path.insert(0, ROOT)
     from oracle import oracle as O
@@ -133,32 +148,117 @@ def cpu_baseline_and_parity(msst, torch, args):
         return (1 + rng.standard_normal(DIM) * 0.02).astype(np.float32)
 
     lw = []
-    for _ in range(2):
+    for _ in range(2 * DEPTH):
         lw.append(dict(attn_gamma=gm(), w_qkv=n(3 * hd, DIM), w_gate=n(HEADS, DIM),
                        b_gate=n(HEADS), w_out=n(DIM, hd), ff_gamma=gm(), w_ff1=n(FF, DIM),
                        b_ff1=n(FF), w_ff2=n(DIM, FF), b_ff2=n(DIM)))
+    fg = gm()
     x = rng.standard_normal((1, FRAMES, BANDS, DIM)).astype(np.float32)
     t0 = time.perf_counter()
-    ref = O.roformer_stack(x, [O.LayerWeights(**w) for w in lw], HEADS, DH, None)
+    ref = O.roformer_stack(x, [O.LayerWeights(**w) for w in lw], HEADS, DH, fg)
     cpu_s = time.perf_counter() - t0
 
     mats = ("w_qkv", "w_gate", "w_out", "w_ff1", "w_ff2")
     dl = [{k: (torch.from_numpy(v).cuda().half() if k in mats else torch.from_numpy(v).cuda())
            for k, v in w.items()} for w in lw]
-    st = msst.RoformerStack(dl, None, 1, FRAMES, BANDS, DIM, HEADS, DH, FF, msst.F16)
+    st = msst.RoformerStack(dl, torch.from_numpy(fg).cuda(), 1, FRAMES, BANDS, DIM, HEADS, DH,
+                            FF, msst.F16)
     xd = torch.from_numpy(x).cuda()
     st(xd)
     torch.cuda.synchronize()
     y = xd.cpu().numpy().astype(np.float64)
     err = float(np.max(np.abs(y - ref)) / np.max(np.abs(ref)))
-    cpu = {"value": round(cpu_s * 1e3 * DEPTH, 1), "unit": "ms/chunk", "cores": threads,
+    cpu = {"value": round(cpu_s * 1e3, 1), "unit": "ms/chunk", "cores": threads,
            "kind": "port",
-           "sample": "fp32 C oracle, one depth (time + frequency transformer) of the "
-                     "12-depth stack at full size [801 frames x 62 bands x 512], "
-                     f"measured {cpu_s:.2f} s, extrapolated x{DEPTH}"}
+           "sample": "fp32 C oracle (OpenMP), one whole 8 s chunk: the 12-depth stack with "
+                     "final norm at full size [801 frames x 62 bands x 512], "
+                     f"measured {cpu_s:.2f} s"}
     parity = {"max_rel_err": err, "tolerance": 2e-2, "metric": "max|y-r|/max|r|",
-              "sample": "same one-depth stack, fp16 HIP path vs fp32 oracle"}
+              "sample": "the same 12-depth chunk, same weights and input: fp16 HIP path vs "
+                        "fp32 oracle"}
     return cpu, parity
+
+
+def ff1_inputs(torch, layers, M):
+    xn = torch.randn(M, DIM, device="cuda",
+                     generator=torch.Generator(device="cuda").manual_seed(2)).half()
+    hid = torch.empty(M, FF, device="cuda", dtype=torch.float16)
+    return xn, hid, layers[0]["w_ff1"], layers[0]["b_ff1"]
+
+
+def pmc_sample(msst, torch, B):
+    """Launch sequence for the counter passes: a plain copy kernel of known
+    size (256 MiB read + 256 MiB written, fp32 negation), then the FF1 GEMM;
+    three launches each, synchronised, nothing else timed."""
+    layers, _ = make_weights(torch, 0, torch.float16)
+    src = torch.randn(64 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    xn, hid, w1, b1 = ff1_inputs(torch, layers, B * FRAMES * BANDS)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        msst.linear(xn, w1, b1, "gelu", out=hid)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_sample": "copy 268435456 B read + 268435456 B written x3; "
+                                    "FF1 GEMM x3"}))
+
+
+def kernel_table(msst, torch, layers, B):
+    """Each kernel of one transformer alone, HIP-event timed on the stream it
+    runs on (50 launches after one warm-up)."""
+    M = B * FRAMES * BANDS
+    hd = HEADS * DH
+    w = layers[0]
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(M, DIM, device="cuda", generator=gen)
+    xn = torch.empty(M, DIM, device="cuda", dtype=torch.float16)
+    gates = torch.empty(M, HEADS, device="cuda")
+    qkv = torch.empty(M, 3 * hd, device="cuda", dtype=torch.float16)
+    merged = torch.empty(M, hd, device="cuda", dtype=torch.float16)
+    hidden = torch.empty(M, FF, device="cuda", dtype=torch.float16)
+    res = torch.randn(M, DIM, device="cuda", generator=gen)
+    tcos, tsin = msst.rope_table_device(FRAMES, DH)
+    fcos, fsin = msst.rope_table_device(BANDS, DH)
+    scale = math.sqrt(DIM)
+    time_l = msst.seq_layout(B * BANDS, 1, FRAMES, FRAMES, 0, 1)
+    freq_l = msst.seq_layout(B, FRAMES, BANDS, BANDS * FRAMES, 1, FRAMES)
+    # (name, fn, flops, bytes) — bytes count each tensor read/written once.
+    ents = [
+        ("rms_norm_gate", lambda: msst.rms_norm_gate(x, w["attn_gamma"], scale, w["w_gate"],
+                                                     w["b_gate"], out=xn, gates=gates),
+         0, M * DIM * (4 + 2) + M * HEADS * 4),
+        ("gemm_qkv_rope", lambda: msst.linear_rope(xn, w["w_qkv"], tcos, tsin, 2 * hd, DH, 1,
+                                                   FRAMES, out=qkv),
+         2.0 * M * DIM * 3 * hd, 2 * M * DIM + 2 * 3 * hd * DIM + 2 * M * 3 * hd),
+        ("attention_time", lambda: msst.gated_rope_attention(qkv, time_l, HEADS, None, None,
+                                                             gates, out=merged),
+         4.0 * B * BANDS * HEADS * FRAMES ** 2 * DH, 2 * M * 3 * hd + 2 * M * hd + 4 * M * HEADS),
+        ("attention_freq", lambda: msst.gated_rope_attention(qkv, freq_l, HEADS, None, None,
+                                                             gates, out=merged),
+         4.0 * B * FRAMES * HEADS * BANDS ** 2 * DH, 2 * M * 3 * hd + 2 * M * hd + 4 * M * HEADS),
+        ("gemm_out_residual", lambda: msst.linear(merged, w["w_out"], residual=res, out=res),
+         2.0 * M * hd * DIM, 2 * M * hd + 2 * DIM * hd + 8 * M * DIM),
+        ("rms_norm", lambda: msst.rms_norm(res, w["ff_gamma"], scale, out=xn),
+         0, M * DIM * (4 + 2)),
+        ("gemm_ff1_gelu", lambda: msst.linear(xn, w["w_ff1"], w["b_ff1"], "gelu", out=hidden),
+         2.0 * M * DIM * FF, 2 * M * DIM + 2 * FF * DIM + 2 * M * FF),
+        ("gemm_ff2_residual", lambda: msst.linear(hidden, w["w_ff2"], w["b_ff2"], residual=res,
+                                                  out=res),
+         2.0 * M * FF * DIM, 2 * M * FF + 2 * DIM * FF + 8 * M * DIM),
+    ]
+    table = {}
+    for name, fn, flops, nbytes in ents:
+        fn()
+        us = time_events(torch, fn, 50) / 50 * 1e3
+        e = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+             "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+        if flops:
+            tf = flops / (us * 1e-6) / 1e12
+            e.update({"tflops": round(tf, 1), "frac_mfma": round(tf / PEAK_F16_TFLOPS, 4)})
+        table[name] = e
+    return table
 
 
 def main():
@@ -168,6 +268,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=1, help="chunks per step (config 5 uses 4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--pmc-sample", action="store_true",
+                    help="run only the copy-kernel calibration and the FF1 GEMM (3 launches "
+                         "each), for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -180,6 +283,9 @@ def main():
     msst.lib()
     torch.manual_seed(0)
     B = args.batch
+    if args.pmc_sample:
+        pmc_sample(msst, torch, B)
+        return
     layers, final_gamma = make_weights(torch, 0, torch.float16)
     st = msst.RoformerStack(layers, final_gamma, B, FRAMES, BANDS, DIM, HEADS, DH, FF, msst.F16)
     x = torch.randn(B, FRAMES, BANDS, DIM, device="cuda",
@@ -195,6 +301,17 @@ def main():
     ms_per_chunk = ms_per_step / B
     assert torch.isfinite(x).all().item(), "non-finite stack output"
 
+    # Host-buffer rate: pinned host chunk -> device, stack, device -> host.
+    xh = torch.empty(B, FRAMES, BANDS, DIM, pin_memory=True)
+    xh.copy_(x.cpu())
+
+    def pcie_step():
+        x.copy_(xh, non_blocking=True)
+        st(x)
+        xh.copy_(x, non_blocking=True)
+    pcie_step()
+    pcie_ms = time_events(torch, pcie_step, 5) / 5 / B
+
     # GEMM replay: the stack's GEMM launches alone.
     run = gemm_replay(msst, torch, layers, B)
     run()
@@ -205,9 +322,7 @@ def main():
     gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
 
     # Dominant kernel: FF1 GEMM (bias + GELU, fp16 out).
-    xn = torch.randn(M, DIM, device="cuda").half()
-    hid = torch.empty(M, FF, device="cuda", dtype=torch.float16)
-    w1, b1 = layers[0]["w_ff1"], layers[0]["b_ff1"]
+    xn, hid, w1, b1 = ff1_inputs(torch, layers, M)
     msst.linear(xn, w1, b1, "gelu", out=hid)
     nl = 50
     ff1_ms = time_events(torch, lambda: msst.linear(xn, w1, b1, "gelu", out=hid), nl) / nl
@@ -243,13 +358,14 @@ def main():
             "chunks_per_step": B, "frames": FRAMES, "bands": BANDS, "dim": DIM, "depth": DEPTH,
         },
         "wall_ms_timed_region": round(wall_ms, 2),
+        "pcie_inclusive_ms_per_chunk": round(pcie_ms, 3),
         "gemm_ms_per_chunk": round(gemm_ms / B, 3),
         "gemm_tflops": round(gemm_tflops, 1),
         "gemm_frac_of_peak": round(gemm_tflops / PEAK_F16_TFLOPS, 4),
         "stack_tflops": round((gemm_flops + attn_flops_chunk(B)) / (ms_per_step * 1e-3) / 1e12, 1),
         "roofline": {
-            "kernel": "gemm_f16_kernel<256,256> FF1 M=49662 K=512 N=2048 bias+GELU fp16 out"
-                      if B == 1 else f"gemm_f16_kernel<256,256> FF1 M={M} K=512 N=2048",
+            "kernel": f"gemm_f16_dma_kernel<256,128,32,3,2,0,half> FF1 M={M} K=512 N=2048 "
+                      "bias+GELU fp16 out",
             "bound": "mfma",
             "achieved": round(ff1_tflops, 1),
             "peak": PEAK_F16_TFLOPS,
@@ -260,6 +376,7 @@ def main():
             "launch_us": round(ff1_ms * 1e3, 2),
         },
     }
+    out["kernels"] = kernel_table(msst, torch, layers, B)
     if not args.no_cpu:
         cpu, parity = cpu_baseline_and_parity(msst, torch, args)
         out["cpu_baseline"] = cpu

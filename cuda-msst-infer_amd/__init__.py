@@ -172,13 +172,15 @@ def rms_norm(x, gamma, scale, out=None, out_dtype=None):
     return out
 
 
-def rms_norm_gate(x, gamma, scale, w_gate, b_gate, out_dtype=None):
+def rms_norm_gate(x, gamma, scale, w_gate, b_gate, out_dtype=None, out=None, gates=None):
     import torch
     D = x.shape[-1]
     rows = x.numel() // D
     G = w_gate.shape[0]
-    out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
-    gates = torch.empty(*x.shape[:-1], G, dtype=torch.float32, device=x.device)
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
+    if gates is None:
+        gates = torch.empty(*x.shape[:-1], G, dtype=torch.float32, device=x.device)
     check(lib().msst_rms_norm_gate(_ptr(x), _dt(x), _ptr(gamma), float(scale), _ptr(out),
                                    _dt(out), _ptr(w_gate), _dt(w_gate), _ptr(b_gate),
                                    _ptr(gates), rows, D, G, _stream()), "msst_rms_norm_gate")
