@@ -27,8 +27,6 @@
 // 8 XCDs, so workgroup b is given tile (b % 8) * per_xcd + b / 8 — every XCD
 // walks a contiguous run of the row-major tile grid and the column tiles of
 // a row block (which share the same A rows) run together in one L2.
-#include <stdlib.h>
-
 #include <type_traits>
 
 #include "msst_common.hpp"
@@ -105,17 +103,26 @@ struct EpiRope {
 
 // Epilogue through LDS.  A wave's (MI*32) x (NI*32) accumulator block is
 // written to its LDS region IP fragment-rows at a time (static register
-// indices), then read back row-contiguously: each lane owns 4 consecutive
+// indices).  TR = false: acc[i][j] = A_i . W_j^T (register v of lane l holds
+// row 8 (v / 4) + 4 h + v % 4, column l % 32), one 4-byte write per value.
+// TR = true: acc[i][j] = W_j . A_i^T, the transposed block (register v holds
+// row l % 32, column 8 (v / 4) + 4 h + v % 4), so every 4 registers are 4
+// consecutive columns of one row: one 16-byte write each, into rows padded
+// by 4 floats so the 16 rows a b128 pass writes fall in distinct banks.
+// Each wave stages through its own region, and a wave's LDS operations
+// execute in order, so no barrier is needed inside the epilogue.
+//
+// The block is read back row-contiguously: each lane owns 4 consecutive
 // columns, so bias is loaded once and global stores are 16-byte (f32) /
 // 8-byte (f16) and row-contiguous.  The read-back runs in batches of U rows
-// per lane: the batch's global loads (residual rows, or RoPE cos/sin rows)
-// first, then its LDS reads, then math and stores — so stores never wait on
-// each other (CDNA counts loads and stores on one vmcnt; a global load
-// inside a rolled loop would make every iteration wait for all earlier
-// stores).  EPI is compile-time for the same reason.  All waves run the
-// same trip counts, so the block barriers are uniform.  Caller: LDS free
-// (after a barrier).
-template <int MI, int NI, int IP, int EPI, typename OutT>
+// per lane, fully unrolled.  The global loads of batch b + 1 (residual
+// rows, or RoPE cos/sin rows) are issued before the stores of batch b: loads
+// and stores share one in-order vmcnt on CDNA, so a load issued after a
+// batch of stores could only be waited for together with those stores.
+// EPI and ACT are compile-time (ACT < 0: the runtime `act` argument).
+// Caller: the wave's region is free (after a barrier that follows the last
+// read of the k-loop's tiles).
+template <int MI, int NI, int IP, int EPI, typename OutT, bool TR = false, int ACT = -1>
 __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds, int lane,
                                                int row0, int col0, int M, int N,
                                                const float* __restrict__ bias, int act,
@@ -123,11 +130,15 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
                                                const EpiRope& rope = EpiRope{}) {
     static_assert(MI % IP == 0, "IP must divide MI");
     constexpr int WN = NI * 32;
+    constexpr int LDW = TR ? WN + 4 : WN;  // LDS row stride (floats)
     constexpr int LPR = WN / 4;    // lanes per row
     constexpr int RPI = 64 / LPR;  // rows per iteration
     constexpr int ITERS = IP * 32 / RPI;
     constexpr int U = ITERS >= 8 ? 8 : ITERS;
     static_assert(ITERS % U == 0, "batch must divide the row count");
+    constexpr int BPP = ITERS / U;        // batches per pass
+    constexpr int NB = (MI / IP) * BPP;   // batches in total
+    constexpr bool LOADS = EPI == kEpiRes || EPI == kEpiRope;
     const int lrow = lane & 31, lh = lane >> 5;
     const int rr = lane / LPR, cq = lane % LPR;
     const int col = col0 + cq * 4;
@@ -143,90 +154,114 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
 #pragma unroll
         for (int e = 0; e < 4; ++e) bv[e] = (col + e < N) ? bias[col + e] : 0.0f;
     }
-#pragma unroll
-    for (int p = 0; p < MI / IP; ++p) {
-#pragma unroll
-        for (int ii = 0; ii < IP; ++ii)
-#pragma unroll
-            for (int j = 0; j < NI; ++j)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int r = ii * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                    wlds[r * WN + j * 32 + lrow] = acc[p * IP + ii][j][v];
-                }
-        __syncthreads();
-        const int prow0 = row0 + p * IP * 32;
-#pragma unroll 1
-        for (int it0 = 0; it0 < ITERS; it0 += U) {
-            f4 rv[U];  // residual values, or (cos, cos, sin, sin) of the 2 pairs
-            if constexpr (EPI == kEpiRes) {
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int grow = prow0 + (it0 + u) * RPI + rr;
-                    const int64_t idx = (int64_t)grow * N + col;
-                    rv[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-                    if (grow < M) {
-                        if (full) {
-                            rv[u] = ld4<OutT>(residual + idx);
-                        } else {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                if (col + e < N) rv[u][e] = (float)residual[idx + e];
-                        }
-                    }
-                }
-            }
-            if constexpr (EPI == kEpiRope) {
-                if (rope_on) {
-#pragma unroll
-                    for (int u = 0; u < U; ++u) {
-                        const int grow = min(prow0 + (it0 + u) * RPI + rr, M - 1);
-                        int rem, pos;
-                        const int q = divmod24(grow, rope.div, rope.inv_div, rem);
-                        divmod24(q, rope.mod, rope.inv_mod, pos);
-                        const int t = pos * (rope.dh >> 1) + pair;
-                        const float2 c = *reinterpret_cast<const float2*>(rope.cos + t);
-                        const float2 sn = *reinterpret_cast<const float2*>(rope.sin + t);
-                        rv[u] = f4{c.x, c.y, sn.x, sn.y};
-                    }
-                }
-            }
-            f4 v[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                v[u] = *reinterpret_cast<const f4*>(wlds + ((it0 + u) * RPI + rr) * WN + cq * 4);
+    auto batch_row = [&](int b, int u) {  // global row of batch b, slot u
+        return row0 + (b / BPP) * IP * 32 + ((b % BPP) * U + u) * RPI + rr;
+    };
+    // rv: residual values, or (cos, cos, sin, sin) of the lane's 2 pairs.
+    auto load_batch = [&](int b, f4 (&rv)[U]) {
+        if constexpr (EPI == kEpiRes) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int grow = prow0 + (it0 + u) * RPI + rr;
+                const int grow = batch_row(b, u);
+                const int64_t idx = (int64_t)grow * N + col;
+                rv[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
                 if (grow < M) {
-                    f4 o;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = act_apply(v[u][e] + bv[e], act);
-                    if constexpr (EPI == kEpiRes) o += rv[u];
-                    if constexpr (EPI == kEpiRope) {
-                        if (rope_on) {
-#pragma unroll
-                            for (int e = 0; e < 2; ++e) {
-                                const float a = (float)(half_t)o[2 * e];
-                                const float b = (float)(half_t)o[2 * e + 1];
-                                const float c = rv[u][e], sn = rv[u][2 + e];
-                                o[2 * e] = a * c - b * sn;
-                                o[2 * e + 1] = a * sn + b * c;
-                            }
-                        }
-                    }
-                    const int64_t idx = (int64_t)grow * N + col;
                     if (full) {
-                        st4<OutT>(out + idx, o);
+                        rv[u] = ld4<OutT>(residual + idx);
                     } else {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            if (col + e < N) out[idx + e] = (OutT)o[e];
+                            if (col + e < N) rv[u][e] = (float)residual[idx + e];
                     }
                 }
             }
+        } else if constexpr (EPI == kEpiRope) {
+            if (rope_on) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int grow = min(batch_row(b, u), M - 1);
+                    int rem, pos;
+                    const int q = divmod24(grow, rope.div, rope.inv_div, rem);
+                    divmod24(q, rope.mod, rope.inv_mod, pos);
+                    const int t = pos * (rope.dh >> 1) + pair;
+                    const float2 c = *reinterpret_cast<const float2*>(rope.cos + t);
+                    const float2 sn = *reinterpret_cast<const float2*>(rope.sin + t);
+                    rv[u] = f4{c.x, c.y, sn.x, sn.y};
+                }
+            }
         }
-        __syncthreads();
+    };
+    f4 rbuf[2][U];
+    if constexpr (LOADS) load_batch(0, rbuf[0]);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int p = b / BPP;
+        if (b % BPP == 0) {
+            // Stage pass p (fragment rows p*IP .. p*IP+IP-1) into the region.
+#pragma unroll
+            for (int ii = 0; ii < IP; ++ii)
+#pragma unroll
+                for (int j = 0; j < NI; ++j) {
+                    if constexpr (TR) {
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            const f16x& a = acc[p * IP + ii][j];
+                            *reinterpret_cast<f4*>(wlds + (ii * 32 + lrow) * LDW + j * 32 +
+                                                   8 * g + 4 * lh) =
+                                f4{a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
+                        }
+                    } else {
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const int r = ii * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                            wlds[r * LDW + j * 32 + lrow] = acc[p * IP + ii][j][v];
+                        }
+                    }
+                }
+        }
+        if constexpr (LOADS) {
+            if (b + 1 < NB) load_batch(b + 1, rbuf[(b + 1) & 1]);
+        }
+        const int it0 = (b % BPP) * U;
+        f4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            v[u] = *reinterpret_cast<const f4*>(wlds + ((it0 + u) * RPI + rr) * LDW + cq * 4);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int grow = batch_row(b, u);
+            if (grow < M) {
+                f4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (ACT >= 0)
+                        o[e] = act_fixed<ACT>(v[u][e] + bv[e]);
+                    else
+                        o[e] = act_apply(v[u][e] + bv[e], act);
+                }
+                if constexpr (EPI == kEpiRes) o += rbuf[b & 1][u];
+                if constexpr (EPI == kEpiRope) {
+                    if (rope_on) {
+                        const f4 cs = rbuf[b & 1][u];
+#pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const float a = (float)(half_t)o[2 * e];
+                            const float bb = (float)(half_t)o[2 * e + 1];
+                            o[2 * e] = a * cs[e] - bb * cs[2 + e];
+                            o[2 * e + 1] = a * cs[2 + e] + bb * cs[e];
+                        }
+                    }
+                }
+                const int64_t idx = (int64_t)grow * N + col;
+                if (full) {
+                    st4<OutT>(out + idx, o);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col + e < N) out[idx + e] = (OutT)o[e];
+                }
+            }
+        }
     }
 }
 
@@ -509,10 +544,13 @@ __device__ __forceinline__ int chunk_swz(int r) {
 
 // BK = 64 (128-byte LDS rows) or 32 (64-byte rows).  NSTG = LDS ring
 // stages: the DMA of k-tile t + NSTG - 1 is issued while tile t computes,
-// so a load has NSTG - 1 k-tiles of MFMA time to land.  MINB = workgroups
-// per CU the register/LDS budget is sized for (two for 256x128 tiles, so
-// one workgroup's epilogue overlaps the other's main loop).
-template <int BM, int BN, int BK, int NSTG, int MINB, int EPI, typename OutT>
+// so a load has NSTG - 1 k-tiles of MFMA time to land.  The per-k-tile
+// barrier is fence-free (lds_barrier): __syncthreads() would add
+// s_waitcnt vmcnt(0) and wait for the younger stages too, serialising the
+// ring.  MINB = workgroups per CU the register/LDS budget is sized for
+// (2 for 256x128 tiles, 3 for 128x128), so one workgroup's prologue and
+// epilogue latency overlaps the others' main loops.
+template <int BM, int BN, int BK, int NSTG, int MINB, int EPI, int ACT, typename OutT>
 __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
     const half_t* __restrict__ A, const half_t* __restrict__ W, const float* __restrict__ bias,
     const OutT* residual, OutT* out, int M, int N, int K, int act, int tiles_n, int per_xcd,
@@ -590,7 +628,7 @@ __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
     for (int kt = 0; kt < KT; ++kt) {
         // k-tile kt has landed once at most the NSTG-2 newer stages remain.
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTG - 2) * INST) : "memory");
-        __syncthreads();
+        lds_barrier();
         const int cur = kt % NSTG;
         const int nslot = (kt + NSTG - 1) % NSTG;  // the slot consumed at kt - 1
         // Past the end the DMA re-fetches the last k-tile into a slot that
@@ -622,7 +660,7 @@ __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
             for (int i = 0; i < MI; ++i) {
 #pragma unroll
                 for (int j = 0; j < NI; ++j)
-                    acc[i][j] = mfma32x32x16(af[kk][i], bf[kk][j], acc[i][j]);
+                    acc[i][j] = mfma32x32x16(bf[kk][j], af[kk][i], acc[i][j]);
 #pragma unroll
                 for (int u = 0; u < PER_G; ++u) {
                     const int idx = (kk * MI + i) * PER_G + u;
@@ -633,218 +671,15 @@ __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    lds_barrier();
 
+    // acc holds the transposed blocks (W_j . A_i^T, see store_tile_lds).
     constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
-    constexpr int kIP = pick_ip<MI, WN, kRegion>();
-    static_assert(kIP * 32 * WN <= kRegion, "epilogue staging does not fit in LDS");
-    store_tile_lds<MI, NI, kIP, EPI, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+    constexpr int kIP = pick_ip<MI, WN + 4, kRegion>();
+    static_assert(kIP * 32 * (WN + 4) <= kRegion, "epilogue staging does not fit in LDS");
+    store_tile_lds<MI, NI, kIP, EPI, OutT, true, ACT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
                                            lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act,
                                            residual, out, vec != 0, rope);
-}
-
-// ---------------------------------------------------------------------------
-// Persistent fp16 GEMM (the production fast path).
-//
-// One workgroup per CU walks a list of output tiles.  Its k-tiles form one
-// continuous stream across tiles: a 3-slot LDS ring (BK = 32) is filled by
-// LDS DMA two k-tiles ahead of the MFMAs, so while tile t's epilogue runs
-// (through a separate LDS staging area) the first k-tiles of tile t+1 are
-// already in flight.  Measured on MI355X: L2 -> LDS streaming saturates at
-// ~75-95 GB/s per CU whatever the depth, so a 256x256 tile (1/128 byte per
-// flop) sits near that limit at full MFMA rate; hiding the epilogue behind
-// the next tile's loads is what the persistent form buys.
-//
-// Ring rows are 64 bytes (4 chunks of 16 B); chunk c of row r is stored at
-// c ^ ((r >> 1) & 3), conflict-free for the 8-row groups of a b128 read.
-// A DMA instruction fills 16 rows: lane l takes row l >> 2, physical chunk
-// l & 3.
-// ---------------------------------------------------------------------------
-template <typename OutT>
-__device__ __forceinline__ void st16(OutT* p, const float* v);
-template <>
-__device__ __forceinline__ void st16<float>(float* p, const float* v) {
-    *reinterpret_cast<f4*>(p) = f4{v[0], v[1], v[2], v[3]};
-}
-template <>
-__device__ __forceinline__ void st16<half_t>(half_t* p, const float* v) {
-    h8 h;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = (half_t)v[e];
-    *reinterpret_cast<h8*>(p) = h;
-}
-
-// Epilogue with 16-byte stores: one 32-row fragment row at a time through
-// the wave's staging area (32 x WN floats), E = 16 / sizeof(OutT) columns
-// per lane.  No global loads: the persistent kernel serves GEMMs without a
-// residual, so stores are never waited on inside the epilogue.
-template <int MI, int NI, typename OutT>
-__device__ __forceinline__ void store_tile16(f16x (&acc)[MI][NI], float* stg, int lane, int row0,
-                                             int col0, int M, int N,
-                                             const float* __restrict__ bias, int act, OutT* out,
-                                             bool vec) {
-    constexpr int WN = NI * 32;
-    constexpr int E = 16 / (int)sizeof(OutT);
-    constexpr int LPR = WN / E;
-    constexpr int RPI = 64 / LPR;
-    constexpr int ITERS = 32 / RPI;
-    const int lrow = lane & 31, lh = lane >> 5;
-    const int rr = lane / LPR, cq = lane % LPR;
-    const int col = col0 + cq * E;
-    const bool full = vec && col0 + WN <= N;  // wave-uniform
-    float bv[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) bv[e] = (bias && col + e < N) ? bias[col + e] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < MI; ++i) {
-#pragma unroll
-        for (int j = 0; j < NI; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                stg[(8 * (v >> 2) + 4 * lh + (v & 3)) * WN + j * 32 + lrow] = acc[i][j][v];
-        __syncthreads();
-        const int irow0 = row0 + i * 32;
-#pragma unroll 2
-        for (int it = 0; it < ITERS; ++it) {
-            const int r = it * RPI + rr;
-            const int grow = irow0 + r;
-            float o[E];
-#pragma unroll
-            for (int e = 0; e < E; e += 4) {
-                f4 t = *reinterpret_cast<const f4*>(stg + r * WN + cq * E + e);
-                o[e] = t[0]; o[e + 1] = t[1]; o[e + 2] = t[2]; o[e + 3] = t[3];
-            }
-#pragma unroll
-            for (int e = 0; e < E; ++e) o[e] = act_apply(o[e] + bv[e], act);
-            if (grow < M) {
-                const int64_t idx = (int64_t)grow * N + col;
-                if (full) {
-                    st16<OutT>(out + idx, o);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < E; ++e)
-                        if (col + e < N) out[idx + e] = (OutT)o[e];
-                }
-            }
-        }
-        __syncthreads();
-    }
-}
-
-template <int BM, int BN, typename OutT>
-__global__ __launch_bounds__(kThreads) void gemm_f16_persist_kernel(
-    const half_t* __restrict__ A, const half_t* __restrict__ W, const float* __restrict__ bias,
-    OutT* out, int M, int N, int K, int act, int tiles_n, int n_tiles, int per_xcd, int vec) {
-    constexpr int BK = 32, NSTG = 3;
-    constexpr int WM = BM / 2, WN = BN / 2;
-    constexpr int MI = WM / 32, NI = WN / 32;
-    constexpr int A_INST = BM * BK * 2 / 1024 / 4;  // 1 KB DMA instructions per wave per stage
-    constexpr int B_INST = BN * BK * 2 / 1024 / 4;
-    constexpr int INST = A_INST + B_INST;
-    constexpr int STAGE = (BM + BN) * BK;  // halves
-    static_assert(A_INST >= 1 && B_INST >= 1, "tile too small");
-    __shared__ __attribute__((aligned(16))) half_t ring[NSTG * STAGE];
-    __shared__ __attribute__((aligned(16))) float stg[4 * 32 * WN];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wid = tid >> 6;
-    const int wm = wid >> 1, wn = wid & 1;
-    const int lrow = lane & 31, lhalf = lane >> 5;
-
-    // This workgroup's tiles: XCD x owns the contiguous run
-    // [x*per_xcd, (x+1)*per_xcd) of the row-major tile grid; the nq
-    // workgroups on it take every nq-th tile of the run.
-    const int x = blockIdx.x & 7, q = blockIdx.x >> 3, nq = gridDim.x >> 3;
-    const int t_begin = x * per_xcd;
-    const int t_end = min(n_tiles, t_begin + per_xcd);
-    const int n_local = t_begin + q < t_end ? (t_end - t_begin - q + nq - 1) / nq : 0;
-    const int KT = K / BK;
-    const int G = n_local * KT;
-    if (G == 0) return;
-
-    const int a_bytes = M * K * 2, b_bytes = N * K * 2;
-    const int sub_row = lane >> 2;
-    const int lchunk = (lane & 3) ^ ((lane >> 3) & 3);
-
-    auto issue = [&](int g) {
-        const int t = t_begin + q + (g / KT) * nq;
-        const int kt = g - (g / KT) * KT;
-        const int tm = t / tiles_n, tn = t - (t / tiles_n) * tiles_n;
-        half_t* As = ring + (g % NSTG) * STAGE;
-        half_t* Bs = As + BM * BK;
-        const int kofs = kt * BK + lchunk * 8;
-#pragma unroll
-        for (int i = 0; i < A_INST; ++i) {
-            const int r = min(tm * BM + (wid * A_INST + i) * 16 + sub_row, M - 1);
-            dma16(A, a_bytes, As + (wid * A_INST + i) * 512, (uint32_t)(r * K + kofs) * 2u);
-        }
-#pragma unroll
-        for (int i = 0; i < B_INST; ++i) {
-            const int r = min(tn * BN + (wid * B_INST + i) * 16 + sub_row, N - 1);
-            dma16(W, b_bytes, Bs + (wid * B_INST + i) * 512, (uint32_t)(r * K + kofs) * 2u);
-        }
-    };
-
-    issue(0);
-    if (G > 1) issue(1);
-
-    for (int jt = 0; jt < n_local; ++jt) {
-        f16x acc[MI][NI];
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-            for (int j = 0; j < NI; ++j) acc[i][j] = f16x{};
-
-        // The k-loop of one tile: the accumulators stay in AGPRs for its
-        // whole length (an epilogue inside the loop body would make the
-        // compiler shuttle them through VGPRs every iteration).
-        for (int kt = 0; kt < KT; ++kt) {
-            const int g = jt * KT + kt;
-            // Stage g must have landed.  Newer outstanding work: DMA g+1
-            // and, at a tile start, the previous tile's epilogue stores
-            // (waited for as well).
-            if (g + 1 < G && kt != 0) {
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(INST) : "memory");
-            } else {
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            }
-            __syncthreads();
-            if (g + 2 < G) issue(g + 2);  // into the slot consumed at g-1
-            const half_t* As = ring + (g % NSTG) * STAGE;
-            const half_t* Bs = As + BM * BK;
-            h8 af[2][MI], bf[2][NI];
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const int c = kk * 2 + lhalf;
-#pragma unroll
-                for (int i = 0; i < MI; ++i) {
-                    const int r = wm * WM + i * 32 + lrow;
-                    af[kk][i] =
-                        *reinterpret_cast<const h8*>(As + r * BK + ((c ^ ((r >> 1) & 3)) << 3));
-                }
-#pragma unroll
-                for (int j = 0; j < NI; ++j) {
-                    const int r = wn * WN + j * 32 + lrow;
-                    bf[kk][j] =
-                        *reinterpret_cast<const h8*>(Bs + r * BK + ((c ^ ((r >> 1) & 3)) << 3));
-                }
-            }
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                for (int i = 0; i < MI; ++i)
-#pragma unroll
-                    for (int j = 0; j < NI; ++j)
-                        acc[i][j] = mfma32x32x16(af[kk][i], bf[kk][j], acc[i][j]);
-            __builtin_amdgcn_iglp_opt(1);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-
-        const int t = t_begin + q + jt * nq;
-        const int tm = t / tiles_n, tn = t - (t / tiles_n) * tiles_n;
-        store_tile16<MI, NI, OutT>(acc, stg + wid * 32 * WN, lane, tm * BM + wm * WM,
-                                   tn * BN + wn * WN, M, N, bias, act, out, vec != 0);
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -939,76 +774,62 @@ int launch_f16(const void* x, bool x_f32, const half_t* w, const float* bias,
     return check_launch("gemm_f16_kernel");
 }
 
+template <int BM, int BN, int BK, int NSTG, int MINB, int EPI, int ACT, typename OutT>
+void launch_dma_epi(const half_t* x, const half_t* w, const float* bias, const OutT* res,
+                    OutT* out, int M, int N, int K, int act, hipStream_t s, const EpiRope& rope) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    int per_xcd;
+    const int grid = num_xcd_slots((int64_t)tiles_m * tiles_n, per_xcd);
+    hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, EPI, ACT, OutT>), dim3(grid),
+                       dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd,
+                       vec_flag(res, out, N), rope);
+}
+
+// The activation is a template parameter of the kernel (its epilogue is
+// straight-line code per activation).
+template <int BM, int BN, int BK, int NSTG, int MINB, int EPI, typename OutT>
+void launch_dma_act(const half_t* x, const half_t* w, const float* bias, const OutT* res,
+                    OutT* out, int M, int N, int K, int act, hipStream_t s, const EpiRope& rope) {
+    switch (act) {
+        case MSST_ACT_GELU:
+            launch_dma_epi<BM, BN, BK, NSTG, MINB, EPI, MSST_ACT_GELU, OutT>(x, w, bias, res, out,
+                                                                             M, N, K, act, s, rope);
+            break;
+        case MSST_ACT_SIGMOID:
+            launch_dma_epi<BM, BN, BK, NSTG, MINB, EPI, MSST_ACT_SIGMOID, OutT>(
+                x, w, bias, res, out, M, N, K, act, s, rope);
+            break;
+        case MSST_ACT_SILU:
+            launch_dma_epi<BM, BN, BK, NSTG, MINB, EPI, MSST_ACT_SILU, OutT>(x, w, bias, res, out,
+                                                                             M, N, K, act, s, rope);
+            break;
+        default:
+            launch_dma_epi<BM, BN, BK, NSTG, MINB, EPI, MSST_ACT_NONE, OutT>(x, w, bias, res, out,
+                                                                             M, N, K, act, s, rope);
+    }
+}
+
 template <int BM, int BN, int BK, int NSTG, int MINB, typename OutT>
 int launch_f16_dma(const half_t* x, const half_t* w, const float* bias, const OutT* res,
                    OutT* out, int M, int N, int K, int act, hipStream_t s,
                    const EpiRope* rope = nullptr) {
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    int per_xcd;
-    int grid = num_xcd_slots((int64_t)tiles_m * tiles_n, per_xcd);
-    const int vec = vec_flag(res, out, N);
     if (rope) {
         if constexpr (std::is_same<OutT, half_t>::value) {
-            hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, kEpiRope, OutT>),
-                               dim3(grid), dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K,
-                               act, tiles_n, per_xcd, vec, *rope);
+            if (act != MSST_ACT_NONE)
+                return set_error(MSST_ERR_UNSUPPORTED, "RoPE epilogue takes no activation");
+            launch_dma_epi<BM, BN, BK, NSTG, MINB, kEpiRope, MSST_ACT_NONE, OutT>(
+                x, w, bias, res, out, M, N, K, act, s, *rope);
         } else {
             return set_error(MSST_ERR_UNSUPPORTED, "RoPE epilogue needs fp16 output");
         }
     } else if (res) {
-        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, kEpiRes, OutT>),
-                           dim3(grid), dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act,
-                           tiles_n, per_xcd, vec, EpiRope{});
+        launch_dma_act<BM, BN, BK, NSTG, MINB, kEpiRes, OutT>(x, w, bias, res, out, M, N, K, act,
+                                                              s, EpiRope{});
     } else {
-        hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, kEpiPlain, OutT>),
-                           dim3(grid), dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act,
-                           tiles_n, per_xcd, vec, EpiRope{});
+        launch_dma_act<BM, BN, BK, NSTG, MINB, kEpiPlain, OutT>(x, w, bias, res, out, M, N, K, act,
+                                                                s, EpiRope{});
     }
     return check_launch("gemm_f16_dma_kernel");
-}
-
-// MSST_GEMM_VARIANT selects among the exact fp16 kernels for A/B timing:
-// 0 = persistent; 1 = 256x256 (N >= 1024) / 256x128 tiles, four BK-32
-// stages; 2 = 256x128 tiles, three BK-32 stages, two workgroups per CU
-// (default: the second workgroup's main loop hides the first one's
-// epilogue); 3 = 256x256 / 256x128 tiles, two BK-64 stages.
-int gemm_variant() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("MSST_GEMM_VARIANT");
-        v = (e && e[0] >= '0' && e[0] <= '3') ? e[0] - '0' : 2;
-    }
-    return v;
-}
-
-int cu_count() {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-            n > 0)
-            cus = n;
-        else
-            cus = 256;
-    }
-    return cus;
-}
-
-template <int BM, int BN, typename OutT>
-int launch_f16_persist(const half_t* x, const half_t* w, const float* bias, OutT* out, int M,
-                       int N, int K, int act, hipStream_t s) {
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    const int n_tiles = tiles_m * tiles_n;
-    const int per_xcd = (n_tiles + 7) / 8;
-    int nq = cu_count() / 8;
-    if (nq < 1) nq = 1;
-    if (nq > per_xcd) nq = per_xcd;
-    const int grid = 8 * nq;
-    hipLaunchKernelGGL((gemm_f16_persist_kernel<BM, BN, OutT>), dim3(grid), dim3(kThreads), 0, s,
-                       x, w, bias, out, M, N, K, act, tiles_n, n_tiles, per_xcd,
-                       vec_flag<OutT>(nullptr, out, N));
-    return check_launch("gemm_f16_persist_kernel");
 }
 
 template <int BM, int BN, typename OutT>
@@ -1073,26 +894,13 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
         if (dma_ok) {
             const half_t* xh = reinterpret_cast<const half_t*>(x);
             const half_t* wh = reinterpret_cast<const half_t*>(w);
-            const int variant = gemm_variant();
-            if (variant == 0 && res == nullptr) {
-                if (N >= 1024)
-                    return launch_f16_persist<256, 256, OutT>(xh, wh, bias, o, m, n, k, act, s);
-                return launch_f16_persist<256, 128, OutT>(xh, wh, bias, o, m, n, k, act, s);
-            }
-            if (variant == 1) {
-                if (N >= 1024)
-                    return launch_f16_dma<256, 256, 32, 4, 1, OutT>(xh, wh, bias, res, o, m, n, k,
-                                                                    act, s);
-                return launch_f16_dma<256, 128, 32, 4, 1, OutT>(xh, wh, bias, res, o, m, n, k, act,
+            // K <= 512: 128 x 128 tiles, three workgroups per CU (a k-loop of
+            // 16 steps leaves prologue / epilogue latency to hide, which
+            // more resident workgroups do); longer K: 256 x 128 tiles, two
+            // per CU (fewer L2 -> LDS bytes per flop).
+            if (k <= 512)
+                return launch_f16_dma<128, 128, 32, 3, 3, OutT>(xh, wh, bias, res, o, m, n, k, act,
                                                                 s);
-            }
-            if (variant == 3) {
-                if (N >= 1024)
-                    return launch_f16_dma<256, 256, 64, 2, 1, OutT>(xh, wh, bias, res, o, m, n, k,
-                                                                    act, s);
-                return launch_f16_dma<256, 128, 64, 2, 1, OutT>(xh, wh, bias, res, o, m, n, k, act,
-                                                                s);
-            }
             return launch_f16_dma<256, 128, 32, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
         }
         const bool vec_ok = (K % 8 == 0) && aligned(x, 16) && aligned(w, 16);
@@ -1168,8 +976,14 @@ extern "C" int msst_linear_rope(const void* x, const void* w, const float* bias,
     r.mod = (int)pos_mod;
     r.inv_div = 1.0f / (float)pos_div;
     r.inv_mod = 1.0f / (float)pos_mod;
-    return launch_f16_dma<256, 128, 32, 3, 2, half_t>(
-        reinterpret_cast<const half_t*>(x), reinterpret_cast<const half_t*>(w), bias, nullptr,
-        reinterpret_cast<half_t*>(out), (int)M, (int)N, (int)K, MSST_ACT_NONE, as_stream(stream),
-        &r);
+    const half_t* xh = reinterpret_cast<const half_t*>(x);
+    const half_t* wh = reinterpret_cast<const half_t*>(w);
+    half_t* oh = reinterpret_cast<half_t*>(out);
+    if (K <= 512)
+        return launch_f16_dma<128, 128, 32, 3, 3, half_t>(xh, wh, bias, nullptr, oh, (int)M, (int)N,
+                                                          (int)K, MSST_ACT_NONE,
+                                                          as_stream(stream), &r);
+    return launch_f16_dma<256, 128, 32, 3, 2, half_t>(xh, wh, bias, nullptr, oh, (int)M, (int)N,
+                                                      (int)K, MSST_ACT_NONE, as_stream(stream),
+                                                      &r);
 }

@@ -68,10 +68,24 @@ __device__ __forceinline__ float erf_as7126(float z) {
     return copysignf(fmaf(-poly, e, 1.0f), z);
 }
 
+// Compile-time activation (ACT = MSST_ACT_*), and the runtime form for
+// kernels that take it as an argument.
+template <int ACT>
+__device__ __forceinline__ float act_fixed(float v) {
+    if constexpr (ACT == MSST_ACT_GELU)
+        return 0.5f * v * (1.0f + erf_as7126(v * 0.70710678118654752f));
+    else if constexpr (ACT == MSST_ACT_SIGMOID)
+        return 1.0f / (1.0f + expf(-v));
+    else if constexpr (ACT == MSST_ACT_SILU)
+        return v / (1.0f + expf(-v));
+    else
+        return v;
+}
+
 __device__ __forceinline__ float act_apply(float v, int act) {
-    if (act == MSST_ACT_GELU) return 0.5f * v * (1.0f + erf_as7126(v * 0.70710678118654752f));
-    if (act == MSST_ACT_SIGMOID) return 1.0f / (1.0f + expf(-v));
-    if (act == MSST_ACT_SILU) return v / (1.0f + expf(-v));
+    if (act == MSST_ACT_GELU) return act_fixed<MSST_ACT_GELU>(v);
+    if (act == MSST_ACT_SIGMOID) return act_fixed<MSST_ACT_SIGMOID>(v);
+    if (act == MSST_ACT_SILU) return act_fixed<MSST_ACT_SILU>(v);
     return v;
 }
 
@@ -94,6 +108,17 @@ __device__ __forceinline__ void dma16(const void* base, int bytes, half_t* lds, 
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voffset, 0, 0, 0);
+}
+
+// Workgroup barrier for LDS hand-offs only.  __syncthreads() carries a
+// workgroup release/acquire fence, which the compiler lowers to
+// s_waitcnt vmcnt(0) before s_barrier: it waits for every outstanding
+// global load, store and LDS DMA of the wave, including DMAs issued for
+// later ring stages and stores that nothing reads back.  Callers of this
+// barrier wait for exactly what the other waves need (their own
+// s_waitcnt vmcnt(N) for DMA stages); LDS reads/writes are drained here.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // q = n / d, r = n % d for 0 <= n < 2^24, d >= 1, inv_d = 1.0f / d: the
