@@ -34,6 +34,8 @@
 // K are staged; the gate (ops_fused.cu:285-303 output) multiplies the
 // normalised output in the epilogue, which writes merged rows
 // out[token, h*64 + d] directly.
+#include <type_traits>
+
 #include "msst_common.hpp"
 
 namespace msst {
@@ -339,13 +341,18 @@ __global__ __launch_bounds__(256) void attn_f16_kernel(AttnParams p) {
 //   then map to distinct banks.
 // Softmax: the score scale folds into the FMA feeding v_exp_f32
 // (s * c - m * c, c = scale * log2 e).  The running max only moves when a
-// block's max exceeds it by more than 8 (log2 units): most blocks skip the
-// rescale of O, and P stays <= 2^8 (exact range for fp16).  Row sums add the
-// fp16 P values the PV MFMA consumes (v_dot2 against 1.0), so numerator and
-// denominator see the same rounding.
-// HPW = 1: 4 waves x 64 queries of one (sequence, head) share double-
-// buffered K/V blocks, each wave DMAs 16 of the 64 rows.  HPW = 4 (<= 64
-// keys): each wave owns one head and DMAs its own single block.
+// half-block's max exceeds it by more than 8 (log2 units): most half-blocks
+// skip the rescale of O, and P stays <= 2^8 (exact range for fp16).  Row
+// sums add the fp16 P values the PV MFMA consumes (v_dot2 against 1.0), so
+// numerator and denominator see the same rounding.  The lane ^ 32 partner
+// of a query's scores is reached with v_permlane32_swap.
+// Schedule: a 64-key block is two 32-key halves.  S of half 1 is issued
+// while the softmax of half 0 runs on the VALU, and PV of half 0 while the
+// softmax of half 1 runs, so MFMA and VALU work of one wave overlap.
+// HPW = 1: 4 waves x 64 queries of one (sequence, head) share a 3-stage K/V
+// ring (each wave DMAs 16 of the 64 rows; fence-free barrier, one block of
+// DMA in flight per wave while a block computes).  HPW = 4 (<= 64 keys):
+// each wave owns one head and DMAs its own single block.
 typedef short s4_t __attribute__((__vector_size__(4 * sizeof(short))));
 typedef __attribute__((address_space(3))) s4_t lds_s4_t;
 
@@ -354,21 +361,45 @@ __device__ __forceinline__ h4 lds_read_tr16(const half_t* ptr) {
     return __builtin_bit_cast(h4, v);
 }
 
+// max over the query's two lanes (l, l ^ 32).
+__device__ __forceinline__ float pair_max(float a) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float a) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// A pointer the compiler can keep in SGPRs (the value is wave-uniform by
+// construction; without this, a descriptor built from it is waterfalled).
+template <typename T>
+__device__ __forceinline__ const T* uniform_ptr(const T* q) {
+    const uint64_t v = reinterpret_cast<uint64_t>(q);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
+}
+
 constexpr float kRescaleLog2 = 8.0f;
 
 template <int HPW>
 __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
     constexpr int WPH = 4 / HPW;
-    constexpr int NSLOT = HPW == 1 ? 2 : 4;
+    constexpr int NSLOT = HPW == 1 ? 3 : 4;
     constexpr int SLOT = 2 * kKB * kD;          // halves: K tile, then V tile
     constexpr int ROWS_W = HPW == 1 ? 16 : 64;  // block rows one wave DMAs
+    constexpr int NDMA = 2 * ROWS_W / 8;        // DMA instructions per wave per block
     __shared__ __attribute__((aligned(16))) half_t lds[NSLOT * SLOT];
 
     int64_t item;
     work_item(p, item);
     if (item >= p.total_items) return;
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lrow = lane & 31, lh = lane >> 5;
     const int head_local = w / WPH, qsub = w % WPH;
     const int head_groups = (p.H + HPW - 1) / HPW;
@@ -397,14 +428,14 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
     // ---- K/V DMA.  Rows past the sequence re-read its last key (masked in
     // the scores, and finite, so P = 0 times V adds exactly 0).
     const int64_t base_off = head_ok ? tok_k(p, seq, 0) * p.ld_in + h * p.head_in : 0;
-    const half_t* kbase = reinterpret_cast<const half_t*>(p.k) + base_off;
-    const half_t* vbase = reinterpret_cast<const half_t*>(p.v) + base_off;
+    const half_t* kbase = uniform_ptr(reinterpret_cast<const half_t*>(p.k) + base_off);
+    const half_t* vbase = uniform_ptr(reinterpret_cast<const half_t*>(p.v) + base_off);
     const uint32_t rsb = (uint32_t)(p.k_pos * p.ld_in * 2);  // bytes between keys
     const int span = (int)((p.n_k - 1) * rsb) + kD * 2;
     const int row0w = HPW == 1 ? w * ROWS_W : 0;
     const int sub = lane >> 3, pch = lane & 7;
     auto slot_ptr = [&](int kb) -> half_t* {
-        return lds + (HPW == 1 ? (kb & 1) : head_local) * SLOT;
+        return lds + (HPW == 1 ? (kb % NSLOT) : head_local) * SLOT;
     };
     auto issue = [&](int kb) {
         half_t* Ks = slot_ptr(kb);
@@ -441,96 +472,120 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
     const float th = kRescaleLog2 / c;
     const h2 ones = h2{(half_t)1.0f, (half_t)1.0f};
 
-    const int nkb = (p.n_k + kKB - 1) / kKB;
-    if (head_ok) issue(0);
-    for (int kb = 0; kb < nkb; ++kb) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        // Slot (kb + 1) & 1 was last read in iteration kb - 1; every wave
-        // has passed the barrier above, so it is free.
-        if (HPW == 1 && kb + 1 < nkb) issue(kb + 1);
-        if (wave_active) {
-            const half_t* Ks = slot_ptr(kb);
-            const half_t* Vs = Ks + kKB * kD;
-            f16x s[2][2];
+    // S^T for the 32 keys of half hf: sh[qt] (keys hf*32 + 8 (v/4) + 4 lh + v%4).
+    auto s_half = [&](const half_t* Ks, int hf, f16x (&shf)[2]) {
+        shf[0] = f16x{};
+        shf[1] = f16x{};
+        const half_t* krow = Ks + (hf * 32 + lrow) * kD;
 #pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) {
-                s[k2][0] = f16x{};
-                s[k2][1] = f16x{};
-                const half_t* krow = Ks + (k2 * 32 + lrow) * kD;
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk) {
-                    const h8 kf =
-                        *reinterpret_cast<const h8*>(krow + (((kk * 2 + lh) ^ kr_sw) << 3));
-                    s[k2][0] = mfma32x32x16(kf, qf[0][kk], s[k2][0]);
-                    s[k2][1] = mfma32x32x16(kf, qf[1][kk], s[k2][1]);
-                }
-            }
-            const int key_base = kb * kKB;
-            const bool tail = key_base + kKB > p.n_k;
-            h8 pf[2][4];
-#pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
-                float mx = -INFINITY;
-#pragma unroll
-                for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        float x = s[k2][qt][v];
-                        if (tail) {
-                            const int key = key_base + k2 * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                            if (key >= p.n_k) x = -INFINITY;
-                            s[k2][qt][v] = x;
-                        }
-                        mx = fmaxf(mx, x);
-                    }
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                if (mx > m_run[qt] + th) {
-                    const float alpha = __builtin_amdgcn_exp2f((m_run[qt] - mx) * c);
-                    m_run[qt] = mx;
-                    l_run[qt] *= alpha;
-#pragma unroll
-                    for (int dm = 0; dm < 2; ++dm)
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) o[qt][dm][v] *= alpha;
-                }
-                const float nmc = -m_run[qt] * c;
-                float ls = 0.0f;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const int k2 = t >> 1, tp = t & 1;
-#pragma unroll
-                    for (int e = 0; e < 8; e += 2) {
-                        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[k2][qt][8 * tp + e], c, nmc));
-                        const float p1 =
-                            __builtin_amdgcn_exp2f(fmaf(s[k2][qt][8 * tp + e + 1], c, nmc));
-                        const h2 pp = h2{(half_t)p0, (half_t)p1};
-                        pf[qt][t][e] = pp[0];
-                        pf[qt][t][e + 1] = pp[1];
-                        ls = __builtin_amdgcn_fdot2(pp, ones, ls, false);
-                    }
-                }
-                l_run[qt] += ls;
-            }
-            // O^T += V^T . P^T, four 16-key substeps.
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-#pragma unroll
-                for (int dm = 0; dm < 2; ++dm) {
-                    const half_t* vp = Vs + t * 16 * kD + voff[dm];
-                    const h4 lo = lds_read_tr16(vp);
-                    const h4 hi = lds_read_tr16(vp + 8 * kD);
-                    const h8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                    o[0][dm] = mfma32x32x16(vf, pf[0][t], o[0][dm]);
-                    o[1][dm] = mfma32x32x16(vf, pf[1][t], o[1][dm]);
-                }
-            }
+        for (int kk = 0; kk < 4; ++kk) {
+            const h8 kf = *reinterpret_cast<const h8*>(krow + (((kk * 2 + lh) ^ kr_sw) << 3));
+            shf[0] = mfma32x32x16(kf, qf[0][kk], shf[0]);
+            shf[1] = mfma32x32x16(kf, qf[1][kk], shf[1]);
         }
-        if (HPW == 4 && kb + 1 < nkb) {
-            // Single-block variant: reached only if a caller forced it onto a
-            // longer sequence; reload this wave's own slot after its reads.
-            __syncthreads();
-            if (head_ok) issue(kb + 1);
+    };
+    // Online softmax of one half: P^T operands pf[qt][tp] (16-key substeps).
+    auto softmax_half = [&](auto tail_c, int key0, f16x (&shf)[2], h8 (&pf)[2][2]) {
+        constexpr bool TAIL = decltype(tail_c)::value;
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            if constexpr (TAIL) {
+                // Register v holds key key0 + 4 lh + 8 (v / 4) + v % 4: one
+                // per-lane limit against immediates (no per-key registers).
+                const int lim = p.n_k - key0 - 4 * lh;
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    if (8 * (v >> 2) + (v & 3) >= lim) shf[qt][v] = -INFINITY;
+            }
+            float m4[4];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4)
+                m4[q4] = fmaxf(fmaxf(shf[qt][4 * q4], shf[qt][4 * q4 + 1]),
+                               fmaxf(shf[qt][4 * q4 + 2], shf[qt][4 * q4 + 3]));
+            const float mx = pair_max(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
+            if (mx > m_run[qt] + th) {
+                const float alpha = __builtin_amdgcn_exp2f((m_run[qt] - mx) * c);
+                m_run[qt] = mx;
+                l_run[qt] *= alpha;
+#pragma unroll
+                for (int dm = 0; dm < 2; ++dm)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) o[qt][dm][v] *= alpha;
+            }
+            const float nmc = -m_run[qt] * c;
+            float ls = 0.0f;
+#pragma unroll
+            for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(shf[qt][8 * tp + e], c, nmc));
+                    const float p1 =
+                        __builtin_amdgcn_exp2f(fmaf(shf[qt][8 * tp + e + 1], c, nmc));
+                    const h2 pp = h2{(half_t)p0, (half_t)p1};
+                    pf[qt][tp][e] = pp[0];
+                    pf[qt][tp][e + 1] = pp[1];
+                    ls = __builtin_amdgcn_fdot2(pp, ones, ls, false);
+                }
+            l_run[qt] += ls;
+        }
+    };
+    // O^T += V^T . P^T over the two 16-key substeps of half hf.
+    auto pv_half = [&](const half_t* Vs, int hf, h8 (&pf)[2][2]) {
+#pragma unroll
+        for (int tp = 0; tp < 2; ++tp)
+#pragma unroll
+            for (int dm = 0; dm < 2; ++dm) {
+                const half_t* vp = Vs + (hf * 2 + tp) * 16 * kD + voff[dm];
+                const h4 lo = lds_read_tr16(vp);
+                const h4 hi = lds_read_tr16(vp + 8 * kD);
+                const h8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                o[0][dm] = mfma32x32x16(vf, pf[0][tp], o[0][dm]);
+                o[1][dm] = mfma32x32x16(vf, pf[1][tp], o[1][dm]);
+            }
+    };
+    auto block = [&](auto tail_c, const half_t* Ks, int key_base) {
+        const half_t* Vs = Ks + kKB * kD;
+        f16x sa[2], sb[2];
+        h8 pa[2][2], pb[2][2];
+        s_half(Ks, 0, sa);
+        s_half(Ks, 1, sb);                      // overlaps softmax of half 0
+        softmax_half(tail_c, key_base, sa, pa);
+        pv_half(Vs, 0, pa);                     // overlaps softmax of half 1
+        softmax_half(tail_c, key_base + 32, sb, pb);
+        pv_half(Vs, 1, pb);
+    };
+
+    const int nkb = (p.n_k + kKB - 1) / kKB;
+    if constexpr (HPW == 1) {
+        // 3-stage ring: blocks kb and kb + 1 in flight before block kb is used.
+        issue(0);
+        if (nkb > 1) issue(1);
+        for (int kb = 0; kb < nkb; ++kb) {
+            if (kb + 1 < nkb)
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA) : "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            // Block kb has landed for every wave; slot (kb + 2) % 3 was last
+            // read in iteration kb - 1, which every wave has finished.
+            lds_barrier();
+            if (kb + 2 < nkb) issue(kb + 2);
+            // Full blocks only here; a partial last block is peeled below so
+            // the masking code does not share this loop's registers.
+            if (wave_active && (kb + 1) * kKB <= p.n_k) block(std::false_type{}, slot_ptr(kb), kb * kKB);
+        }
+        if (wave_active && nkb * kKB > p.n_k)
+            block(std::true_type{}, slot_ptr(nkb - 1), (nkb - 1) * kKB);
+    } else {
+        // One block per wave, in the wave's own slot: the host selects this
+        // variant only for sequences of at most 64 keys (launch_attention).
+        if (head_ok) issue(0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        lds_barrier();
+        if (wave_active) {
+            if (p.n_k < kKB)
+                block(std::true_type{}, slot_ptr(0), 0);
+            else
+                block(std::false_type{}, slot_ptr(0), 0);
         }
     }
 
@@ -539,7 +594,7 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         const int qi = q0 + qt * 32 + lrow;
-        const float l_tot = l_run[qt] + __shfl_xor(l_run[qt], 32, 64);
+        const float l_tot = pair_sum(l_run[qt]);
         if (qi >= p.n_q) continue;
         const int64_t tok = tok_q(p, seq, qi);
         float scale = 1.0f / l_tot;
