@@ -548,20 +548,23 @@ __device__ __forceinline__ int chunk_swz(int r) {
 // barrier is fence-free (lds_barrier): __syncthreads() would add
 // s_waitcnt vmcnt(0) and wait for the younger stages too, serialising the
 // ring.  MINB = workgroups per CU the register/LDS budget is sized for
-// (2 for 256x128 tiles, 3 for 128x128), so one workgroup's prologue and
-// epilogue latency overlaps the others' main loops.
-template <int BM, int BN, int BK, int NSTG, int MINB, int EPI, int ACT, typename OutT>
-__global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
+// (3 for 128x128 tiles, so one workgroup's prologue and epilogue latency
+// overlaps the others' main loops; 1 for the 8-wave 256x256 tile).  NWN =
+// waves along N (2 x NWN waves, each owning a (BM/2) x (BN/NWN) sub-tile).
+template <int BM, int BN, int BK, int NSTG, int MINB, int NWN, int EPI, int ACT, typename OutT>
+__global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
     const half_t* __restrict__ A, const half_t* __restrict__ W, const float* __restrict__ bias,
     const OutT* residual, OutT* out, int M, int N, int K, int act, int tiles_n, int per_xcd,
     int vec, EpiRope rope) {
     constexpr int CPR = BK / 8;              // 16-byte chunks per LDS row
     constexpr int RPD = 64 / CPR;            // rows per 1 KB DMA instruction
     constexpr int KK = BK / 16;              // MFMA k-substeps per k-tile
-    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int NW = 2 * NWN;              // waves: 2 along M x NWN along N
+    constexpr int WM = BM / 2, WN = BN / NWN;
     constexpr int MI = WM / 32, NI = WN / 32;
-    constexpr int A_INST = BM / RPD / 4;     // DMA instructions per wave per k-tile
-    constexpr int B_INST = BN / RPD / 4;
+    constexpr int A_INST = BM / RPD / NW;    // DMA instructions per wave per k-tile
+    constexpr int B_INST = BN / RPD / NW;
+    static_assert(A_INST * RPD * NW == BM && B_INST * RPD * NW == BN, "DMA split");
     constexpr int STAGE = (BM + BN) * BK;    // halves per LDS buffer
     static_assert(A_INST >= 1 && B_INST >= 1, "tile too small for the DMA split");
     static_assert(NSTG >= 2 && (NSTG - 2) * (A_INST + B_INST) <= 63, "vmcnt range");
@@ -574,7 +577,7 @@ __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wid = tid >> 6;
-    const int wm = wid >> 1, wn = wid & 1;
+    const int wm = wid / NWN, wn = wid % NWN;
     const int lrow = lane & 31, lhalf = lane >> 5;
 
     const int a_bytes = M * K * 2, b_bytes = N * K * 2;
@@ -674,7 +677,7 @@ __global__ __launch_bounds__(kThreads, MINB) void gemm_f16_dma_kernel(
     lds_barrier();
 
     // acc holds the transposed blocks (W_j . A_i^T, see store_tile_lds).
-    constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
+    constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / NW);
     constexpr int kIP = pick_ip<MI, WN + 4, kRegion>();
     static_assert(kIP * 32 * (WN + 4) <= kRegion, "epilogue staging does not fit in LDS");
     store_tile_lds<MI, NI, kIP, EPI, OutT, true, ACT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
@@ -774,42 +777,42 @@ int launch_f16(const void* x, bool x_f32, const half_t* w, const float* bias,
     return check_launch("gemm_f16_kernel");
 }
 
-template <int BM, int BN, int BK, int NSTG, int MINB, int EPI, int ACT, typename OutT>
+template <int BM, int BN, int BK, int NSTG, int MINB, int NWN, int EPI, int ACT, typename OutT>
 void launch_dma_epi(const half_t* x, const half_t* w, const float* bias, const OutT* res,
                     OutT* out, int M, int N, int K, int act, hipStream_t s, const EpiRope& rope) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int per_xcd;
     const int grid = num_xcd_slots((int64_t)tiles_m * tiles_n, per_xcd);
-    hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, EPI, ACT, OutT>), dim3(grid),
-                       dim3(kThreads), 0, s, x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd,
+    hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, NWN, EPI, ACT, OutT>),
+                       dim3(grid), dim3(128 * NWN), 0, s, x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd,
                        vec_flag(res, out, N), rope);
 }
 
 // The activation is a template parameter of the kernel (its epilogue is
 // straight-line code per activation).
-template <int BM, int BN, int BK, int NSTG, int MINB, int EPI, typename OutT>
+template <int BM, int BN, int BK, int NSTG, int MINB, int NWN, int EPI, typename OutT>
 void launch_dma_act(const half_t* x, const half_t* w, const float* bias, const OutT* res,
                     OutT* out, int M, int N, int K, int act, hipStream_t s, const EpiRope& rope) {
     switch (act) {
         case MSST_ACT_GELU:
-            launch_dma_epi<BM, BN, BK, NSTG, MINB, EPI, MSST_ACT_GELU, OutT>(x, w, bias, res, out,
+            launch_dma_epi<BM, BN, BK, NSTG, MINB, NWN, EPI, MSST_ACT_GELU, OutT>(x, w, bias, res, out,
                                                                              M, N, K, act, s, rope);
             break;
         case MSST_ACT_SIGMOID:
-            launch_dma_epi<BM, BN, BK, NSTG, MINB, EPI, MSST_ACT_SIGMOID, OutT>(
+            launch_dma_epi<BM, BN, BK, NSTG, MINB, NWN, EPI, MSST_ACT_SIGMOID, OutT>(
                 x, w, bias, res, out, M, N, K, act, s, rope);
             break;
         case MSST_ACT_SILU:
-            launch_dma_epi<BM, BN, BK, NSTG, MINB, EPI, MSST_ACT_SILU, OutT>(x, w, bias, res, out,
+            launch_dma_epi<BM, BN, BK, NSTG, MINB, NWN, EPI, MSST_ACT_SILU, OutT>(x, w, bias, res, out,
                                                                              M, N, K, act, s, rope);
             break;
         default:
-            launch_dma_epi<BM, BN, BK, NSTG, MINB, EPI, MSST_ACT_NONE, OutT>(x, w, bias, res, out,
+            launch_dma_epi<BM, BN, BK, NSTG, MINB, NWN, EPI, MSST_ACT_NONE, OutT>(x, w, bias, res, out,
                                                                              M, N, K, act, s, rope);
     }
 }
 
-template <int BM, int BN, int BK, int NSTG, int MINB, typename OutT>
+template <int BM, int BN, int BK, int NSTG, int MINB, int NWN, typename OutT>
 int launch_f16_dma(const half_t* x, const half_t* w, const float* bias, const OutT* res,
                    OutT* out, int M, int N, int K, int act, hipStream_t s,
                    const EpiRope* rope = nullptr) {
@@ -817,16 +820,16 @@ int launch_f16_dma(const half_t* x, const half_t* w, const float* bias, const Ou
         if constexpr (std::is_same<OutT, half_t>::value) {
             if (act != MSST_ACT_NONE)
                 return set_error(MSST_ERR_UNSUPPORTED, "RoPE epilogue takes no activation");
-            launch_dma_epi<BM, BN, BK, NSTG, MINB, kEpiRope, MSST_ACT_NONE, OutT>(
+            launch_dma_epi<BM, BN, BK, NSTG, MINB, NWN, kEpiRope, MSST_ACT_NONE, OutT>(
                 x, w, bias, res, out, M, N, K, act, s, *rope);
         } else {
             return set_error(MSST_ERR_UNSUPPORTED, "RoPE epilogue needs fp16 output");
         }
     } else if (res) {
-        launch_dma_act<BM, BN, BK, NSTG, MINB, kEpiRes, OutT>(x, w, bias, res, out, M, N, K, act,
+        launch_dma_act<BM, BN, BK, NSTG, MINB, NWN, kEpiRes, OutT>(x, w, bias, res, out, M, N, K, act,
                                                               s, EpiRope{});
     } else {
-        launch_dma_act<BM, BN, BK, NSTG, MINB, kEpiPlain, OutT>(x, w, bias, res, out, M, N, K, act,
+        launch_dma_act<BM, BN, BK, NSTG, MINB, NWN, kEpiPlain, OutT>(x, w, bias, res, out, M, N, K, act,
                                                                 s, EpiRope{});
     }
     return check_launch("gemm_f16_dma_kernel");
@@ -894,14 +897,15 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
         if (dma_ok) {
             const half_t* xh = reinterpret_cast<const half_t*>(x);
             const half_t* wh = reinterpret_cast<const half_t*>(w);
-            // K <= 512: 128 x 128 tiles, three workgroups per CU (a k-loop of
-            // 16 steps leaves prologue / epilogue latency to hide, which
-            // more resident workgroups do); longer K: 256 x 128 tiles, two
-            // per CU (fewer L2 -> LDS bytes per flop).
-            if (k <= 512)
-                return launch_f16_dma<128, 128, 32, 3, 3, OutT>(xh, wh, bias, res, o, m, n, k, act,
-                                                                s);
-            return launch_f16_dma<256, 128, 32, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
+            // Tile choice (measured on the Roformer shapes): with an
+            // activation the epilogue is VALU-heavy and 128 x 128 tiles at
+            // three workgroups per CU hide it behind the others' main loops;
+            // otherwise one 256 x 256 tile per CU (8 waves) moves the fewest
+            // L2 -> LDS bytes per flop, which bounds these GEMMs.
+            if (act != MSST_ACT_NONE)
+                return launch_f16_dma<128, 128, 32, 3, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act,
+                                                                   s);
+            return launch_f16_dma<256, 256, 32, 3, 1, 4, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
         }
         const bool vec_ok = (K % 8 == 0) && aligned(x, 16) && aligned(w, 16);
         if (!vec_ok)
@@ -979,11 +983,7 @@ extern "C" int msst_linear_rope(const void* x, const void* w, const float* bias,
     const half_t* xh = reinterpret_cast<const half_t*>(x);
     const half_t* wh = reinterpret_cast<const half_t*>(w);
     half_t* oh = reinterpret_cast<half_t*>(out);
-    if (K <= 512)
-        return launch_f16_dma<128, 128, 32, 3, 3, half_t>(xh, wh, bias, nullptr, oh, (int)M, (int)N,
-                                                          (int)K, MSST_ACT_NONE,
-                                                          as_stream(stream), &r);
-    return launch_f16_dma<256, 128, 32, 3, 2, half_t>(xh, wh, bias, nullptr, oh, (int)M, (int)N,
-                                                      (int)K, MSST_ACT_NONE, as_stream(stream),
-                                                      &r);
+    return launch_f16_dma<256, 256, 32, 3, 1, 4, half_t>(xh, wh, bias, nullptr, oh, (int)M,
+                                                         (int)N, (int)K, MSST_ACT_NONE,
+                                                         as_stream(stream), &r);
 }
