@@ -356,16 +356,30 @@ __global__ __launch_bounds__(256) void attn_f16_kernel(AttnParams p) {
 typedef short s4_t __attribute__((__vector_size__(4 * sizeof(short))));
 typedef __attribute__((address_space(3))) s4_t lds_s4_t;
 
-__device__ __forceinline__ h4 lds_read_tr16(const half_t* ptr) {
-    const s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)(const_cast<half_t*>(ptr)));
+__device__ __forceinline__ h4 lds_read_tr16(const lds_half_t* ptr) {
+    const s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)(ptr));
     return __builtin_bit_cast(h4, v);
+}
+
+// Plain v_max: the scores come from MFMA accumulators (never signalling
+// NaNs), and fmaxf in IEEE mode would first canonicalise every input with
+// an extra v_max x, x.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float vmax(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
 }
 
 // max over the query's two lanes (l, l ^ 32).
 __device__ __forceinline__ float pair_max(float a) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false,
                                                     false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float pair_sum(float a) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false,
@@ -434,12 +448,13 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
     const int span = (int)((p.n_k - 1) * rsb) + kD * 2;
     const int row0w = HPW == 1 ? w * ROWS_W : 0;
     const int sub = lane >> 3, pch = lane & 7;
-    auto slot_ptr = [&](int kb) -> half_t* {
-        return lds + (HPW == 1 ? (kb % NSLOT) : head_local) * SLOT;
+    lds_half_t* const L = (lds_half_t*)lds;
+    auto slot_ptr = [&](int kb) -> lds_half_t* {
+        return L + (HPW == 1 ? (kb % NSLOT) : head_local) * SLOT;
     };
     auto issue = [&](int kb) {
-        half_t* Ks = slot_ptr(kb);
-        half_t* Vs = Ks + kKB * kD;
+        lds_half_t* Ks = slot_ptr(kb);
+        lds_half_t* Vs = Ks + kKB * kD;
 #pragma unroll
         for (int i = 0; i < ROWS_W / 8; ++i) {
             const int r = row0w + i * 8 + sub;
@@ -450,16 +465,21 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
         }
     };
 
-    // Per-lane parts of the fragment addresses.
+    // Per-lane byte offsets of the fragment reads within a slot (the XOR
+    // swizzles make them lane-dependent; everything else is an immediate).
     const int kr_sw = (lrow >> 1) & 7;
+    int kofs[4];  // halves
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) kofs[kk] = lrow * kD + (((kk * 2 + lh) ^ kr_sw) << 3);
     const int g = lane >> 4, j16 = lane & 15;
     const int vrow = 4 * (g >> 1) + (j16 >> 2);  // row within an 8-key group
     const int vsw = ((vrow >> 1) & 1) << 2;
     const int vch = 2 * (g & 1) + ((j16 & 3) >> 1);
     const int vsub = (j16 & 1) * 4;
-    int voff[2];
+    int voff[2];  // halves, from the slot start (V tile follows the K tile)
 #pragma unroll
-    for (int dm = 0; dm < 2; ++dm) voff[dm] = vrow * kD + (((4 * dm + vch) ^ vsw) << 3) + vsub;
+    for (int dm = 0; dm < 2; ++dm)
+        voff[dm] = kKB * kD + vrow * kD + (((4 * dm + vch) ^ vsw) << 3) + vsub;
 
     f16x o[2][2];
 #pragma unroll
@@ -473,13 +493,12 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
     const h2 ones = h2{(half_t)1.0f, (half_t)1.0f};
 
     // S^T for the 32 keys of half hf: sh[qt] (keys hf*32 + 8 (v/4) + 4 lh + v%4).
-    auto s_half = [&](const half_t* Ks, int hf, f16x (&shf)[2]) {
+    auto s_half = [&](const lds_half_t* Ks, int hf, f16x (&shf)[2]) {
         shf[0] = f16x{};
         shf[1] = f16x{};
-        const half_t* krow = Ks + (hf * 32 + lrow) * kD;
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            const h8 kf = *reinterpret_cast<const h8*>(krow + (((kk * 2 + lh) ^ kr_sw) << 3));
+            const h8 kf = *(const lds_h8_t*)(Ks + kofs[kk] + hf * 32 * kD);
             shf[0] = mfma32x32x16(kf, qf[0][kk], shf[0]);
             shf[1] = mfma32x32x16(kf, qf[1][kk], shf[1]);
         }
@@ -497,12 +516,10 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
                 for (int v = 0; v < 16; ++v)
                     if (8 * (v >> 2) + (v & 3) >= lim) shf[qt][v] = -INFINITY;
             }
-            float m4[4];
+            float m = vmax3(shf[qt][0], shf[qt][1], shf[qt][2]);
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4)
-                m4[q4] = fmaxf(fmaxf(shf[qt][4 * q4], shf[qt][4 * q4 + 1]),
-                               fmaxf(shf[qt][4 * q4 + 2], shf[qt][4 * q4 + 3]));
-            const float mx = pair_max(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
+            for (int v = 3; v < 15; v += 2) m = vmax3(m, shf[qt][v], shf[qt][v + 1]);
+            const float mx = pair_max(vmax(m, shf[qt][15]));
             if (mx > m_run[qt] + th) {
                 const float alpha = __builtin_amdgcn_exp2f((m_run[qt] - mx) * c);
                 m_run[qt] = mx;
@@ -530,12 +547,12 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
         }
     };
     // O^T += V^T . P^T over the two 16-key substeps of half hf.
-    auto pv_half = [&](const half_t* Vs, int hf, h8 (&pf)[2][2]) {
+    auto pv_half = [&](const lds_half_t* Ks, int hf, h8 (&pf)[2][2]) {
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp)
 #pragma unroll
             for (int dm = 0; dm < 2; ++dm) {
-                const half_t* vp = Vs + (hf * 2 + tp) * 16 * kD + voff[dm];
+                const lds_half_t* vp = Ks + voff[dm] + (hf * 2 + tp) * 16 * kD;
                 const h4 lo = lds_read_tr16(vp);
                 const h4 hi = lds_read_tr16(vp + 8 * kD);
                 const h8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -543,16 +560,15 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
                 o[1][dm] = mfma32x32x16(vf, pf[1][tp], o[1][dm]);
             }
     };
-    auto block = [&](auto tail_c, const half_t* Ks, int key_base) {
-        const half_t* Vs = Ks + kKB * kD;
+    auto block = [&](auto tail_c, const lds_half_t* Ks, int key_base) {
         f16x sa[2], sb[2];
         h8 pa[2][2], pb[2][2];
         s_half(Ks, 0, sa);
         s_half(Ks, 1, sb);                      // overlaps softmax of half 0
         softmax_half(tail_c, key_base, sa, pa);
-        pv_half(Vs, 0, pa);                     // overlaps softmax of half 1
+        pv_half(Ks, 0, pa);                     // overlaps softmax of half 1
         softmax_half(tail_c, key_base + 32, sb, pb);
-        pv_half(Vs, 1, pb);
+        pv_half(Ks, 1, pb);
     };
 
     const int nkb = (p.n_k + kKB - 1) / kKB;

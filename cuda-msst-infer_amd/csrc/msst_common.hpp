@@ -110,6 +110,19 @@ __device__ __forceinline__ void dma16(const void* base, int bytes, half_t* lds, 
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voffset, 0, 0, 0);
 }
 
+// LDS-typed (address space 3) pointers: 32-bit LDS addresses, so address
+// arithmetic folds into ds_* immediates instead of per-access conversions
+// from generic pointers.
+typedef __attribute__((address_space(3))) half_t lds_half_t;
+typedef __attribute__((address_space(3))) h8 lds_h8_t;
+
+__device__ __forceinline__ void dma16(const void* base, int bytes, lds_half_t* lds,
+                                      uint32_t voffset) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voffset, 0, 0, 0);
+}
+
 // Workgroup barrier for LDS hand-offs only.  __syncthreads() carries a
 // workgroup release/acquire fence, which the compiler lowers to
 // s_waitcnt vmcnt(0) before s_barrier: it waits for every outstanding
