@@ -59,6 +59,14 @@ class StackDesc(ctypes.Structure):
         ("w_dtype", _int)]
 
 
+class BandConfig(ctypes.Structure):
+    _fields_ = [("num_bands", _int), ("band_dims", ctypes.POINTER(_int)), ("dim", _int),
+                ("hidden", _int), ("mlp_linears", _int)]
+
+
+_BCP = ctypes.POINTER(BandConfig)
+_PP = ctypes.POINTER(_vp)
+
 _SIGS = {
     "msst_abi_version": ([], _int),
     "msst_status_string": ([_int], ctypes.c_char_p),
@@ -83,6 +91,12 @@ _SIGS = {
     "msst_roformer_stack_workspace": ([ctypes.POINTER(StackDesc)], _i64),
     "msst_roformer_stack": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights), _vp,
                              _vp, _i64, _vp], _int),
+    "msst_band_plan_bytes": ([_BCP], _i64),
+    "msst_band_plan_init": ([_BCP, _PP, _PP, _PP, _PP, _PP, _vp, _i64, _vp], _int),
+    "msst_band_split_workspace": ([_BCP, _i64], _i64),
+    "msst_band_split": ([_BCP, _vp, _vp, _i64, _vp, _vp, _i64, _vp], _int),
+    "msst_mask_estimator_workspace": ([_BCP, _i64], _i64),
+    "msst_mask_estimator": ([_BCP, _vp, _vp, _int, _i64, _vp, _vp, _i64, _vp], _int),
     "msst_roformer_transformer": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights),
                                    _int, _vp, _i64, _vp], _int),
 }
@@ -329,3 +343,65 @@ class RoformerStack:
             _ptr(self.workspace), self.workspace.numel(), _stream()),
             "msst_roformer_transformer")
         return x
+
+
+class BandPlan:
+    """Device plan of the band split and/or one stem's mask estimator
+    (msst_band_plan_init).  dims: features per band; split = (gammas, ws,
+    biases) per band; mask = (ws, biases) per band, each a list of the L
+    linears.  Keeps references to every tensor it points at."""
+
+    def __init__(self, dims, dim, split=None, mask=None, hidden=0):
+        import torch
+        self.dims = [int(d) for d in dims]
+        self._dims_c = (_int * len(self.dims))(*self.dims)
+        L = len(mask[0][0]) if mask is not None else 1
+        if mask is not None and L > 1:
+            hidden = mask[0][0][0].shape[0]
+        self.cfg = BandConfig(len(self.dims), self._dims_c, int(dim), int(hidden), int(L))
+        nbytes = lib().msst_band_plan_bytes(ctypes.byref(self.cfg))
+        if nbytes < 0:
+            check(-2, "msst_band_plan_bytes")
+        self.plan = torch.empty(int(nbytes), dtype=torch.uint8, device="cuda")
+        self._keep = []
+
+        def arr(ts):
+            if ts is None:
+                return None
+            self._keep.extend(ts)
+            return (_vp * len(ts))(*[t.data_ptr() for t in ts])
+
+        sg = sw = sb = mw = mb = None
+        if split is not None:
+            sg, sw, sb = (arr(list(x)) for x in split)
+        if mask is not None:
+            mw = arr([w for band in mask[0] for w in band])
+            mb = arr([b for band in mask[1] for b in band])
+        check(lib().msst_band_plan_init(ctypes.byref(self.cfg), sg, sw, sb, mw, mb,
+                                        _ptr(self.plan), nbytes, _stream()),
+              "msst_band_plan_init")
+
+    def band_split(self, x, out=None):
+        """x f32 [rows, sum(dims)] -> f32 [rows, nb, dim]."""
+        import torch
+        rows = x.shape[0]
+        if out is None:
+            out = torch.empty(rows, len(self.dims), self.cfg.dim, device=x.device)
+        wsb = lib().msst_band_split_workspace(ctypes.byref(self.cfg), rows)
+        ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=x.device)
+        check(lib().msst_band_split(ctypes.byref(self.cfg), _ptr(self.plan), _ptr(x), rows,
+                                    _ptr(out), _ptr(ws), wsb, _stream()), "msst_band_split")
+        return out
+
+    def mask_estimator(self, x, out=None):
+        """x f32/f16 [rows, nb, dim] -> f32 [rows, sum(dims)]."""
+        import torch
+        rows = x.shape[0]
+        if out is None:
+            out = torch.empty(rows, sum(self.dims), device=x.device)
+        wsb = lib().msst_mask_estimator_workspace(ctypes.byref(self.cfg), rows)
+        ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=x.device)
+        check(lib().msst_mask_estimator(ctypes.byref(self.cfg), _ptr(self.plan), _ptr(x), _dt(x),
+                                        rows, _ptr(out), _ptr(ws), wsb, _stream()),
+              "msst_mask_estimator")
+        return out

@@ -1,0 +1,580 @@
+// bands.hip — the band split and the mask estimator of the Roformer models
+// as grouped kernels.
+//
+// The reference runs both as a host loop over the bands (BSRoformer
+// model_bs_roformer.cu:337-368 and :374-414; MelBandRoformer
+// model_mel_band_roformer.cu:658-690 and :696-738): per band an rms_norm and
+// a linear (band split), or a linear -> tanh -> ... -> linear chain and a
+// glu (mask estimator), then stack / cat.  With 60-62 bands of 801 tokens
+// each, every one of those GEMMs is a handful of tiles, so here each layer
+// is ONE launch over all bands:
+//
+//   band_norm_kernel     segmented RMSNorm: band b of every token row,
+//                        scaled by sqrt(dims[b]), written as fp16 and
+//                        zero-padded to a multiple of 64 columns (the fp16
+//                        rounding is the cast ops::linear applies to its
+//                        input, ops_linear.cu:155).
+//   band_gemm_kernel     grouped MFMA GEMM (LDS DMA ring, 128 x 128 tiles),
+//                        one group per band; the tile -> band map is a scan
+//                        over the bands' tile counts.  Epilogues:
+//                          kSplit   out[r, b, :] = acc + bias_b       (fp32)
+//                          kHidden  tanh(acc + bias)                  (fp16)
+//                          kGlu     v[m] * sigmoid(v[m + d])          (fp32)
+//                        For kGlu the W rows are read interleaved (tile row
+//                        2m is W row m, 2m + 1 is W row m + d), so each GLU
+//                        pair lands in adjacent columns of one lane.
+//
+// Per-band weights stay in the caller's tensors: msst_band_plan_init copies
+// their addresses and the band offsets into a device-resident plan once per
+// model (and packs the band-split weights, whose widths are not multiples of
+// the 64-column k-slice, into zero-padded rows).  The per-chunk calls read
+// the plan with scalar loads.
+#include <algorithm>
+#include <cstring>
+
+#include "msst_common.hpp"
+
+namespace msst {
+namespace {
+
+constexpr int kMaxBands = 64;
+constexpr int kMaxLinears = 8;
+
+struct BandPlan {
+    int nb, dim, hid, L;
+    int ftot;        // sum of dims
+    int kpad_total;  // sum of kpad
+    int has_split, has_mask;
+    int fd[kMaxBands];    // features of band b (2 * freqs * channels)
+    int foff[kMaxBands];  // first feature column of band b
+    int kpad[kMaxBands];  // fd rounded up to 64
+    int koff[kMaxBands];  // first column of band b in the padded layout
+    const float* split_gamma[kMaxBands];
+    const half_t* split_w[kMaxBands];  // caller's W_b [dim, fd_b], read once by the packer
+    const float* split_b[kMaxBands];
+    const half_t* mask_w[kMaxBands * kMaxLinears];
+    const float* mask_b[kMaxBands * kMaxLinears];
+};
+// The packed band-split weights follow the plan header: band b is
+// [dim][kpad_b] halves at element offset dim * koff_b.
+constexpr int64_t kPlanHeader = (sizeof(BandPlan) + 255) / 256 * 256;
+
+__device__ __forceinline__ const half_t* packed_w(const BandPlan* p) {
+    return reinterpret_cast<const half_t*>(reinterpret_cast<const char*>(p) + kPlanHeader);
+}
+
+// ---------------------------------------------------------------------------
+// W_b [dim, fd_b] -> packed [dim, kpad_b], zero beyond fd_b.  One thread per
+// packed element; grid-stride over all bands.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void band_pack_kernel(BandPlan* plan, int nb, int dim,
+                                                        int64_t total) {
+    half_t* dst = reinterpret_cast<half_t*>(reinterpret_cast<char*>(plan) + kPlanHeader);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        // Find the band of packed element i (bands are few; linear scan).
+        int b = 0;
+        while (b + 1 < nb && i >= (int64_t)dim * plan->koff[b + 1]) ++b;
+        const int64_t local = i - (int64_t)dim * plan->koff[b];
+        const int kp = plan->kpad[b], fd = plan->fd[b];
+        const int n = (int)(local / kp), k = (int)(local % kp);
+        dst[i] = k < fd ? plan->split_w[b][(int64_t)n * fd + k] : (half_t)0.0f;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Segmented RMSNorm: one wave per (token row, band).
+//   y[r, koff_b + j] = fp16(x[r, foff_b + j] * rsqrt(sum_j x^2 + 1e-12)
+//                            * gamma_b[j] * sqrt(fd_b)),   0 for fd_b <= j < kpad_b
+// (ops_norm.cu:85-111 with scale = sqrt(band dim), model_bs_roformer.cu:357).
+// ---------------------------------------------------------------------------
+constexpr int kNormMaxPerLane = 16;  // fd <= 1024
+
+__global__ __launch_bounds__(256) void band_norm_kernel(const BandPlan* __restrict__ plan,
+                                                        const float* __restrict__ x, int rows,
+                                                        half_t* __restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nb = plan->nb;
+    const int row = (int)(gw / nb), b = (int)(gw % nb);
+    if (row >= rows) return;
+    const int fd = plan->fd[b], kp = plan->kpad[b];
+    const float* xr = x + (int64_t)row * plan->ftot + plan->foff[b];
+    const float* g = plan->split_gamma[b];
+    float v[kNormMaxPerLane];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormMaxPerLane; ++i) {
+        const int j = lane + 64 * i;
+        v[i] = j < fd ? xr[j] : 0.0f;
+        ss = fmaf(v[i], v[i], ss);
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss + 1e-12f);
+    const float scale = sqrtf((float)fd);
+    half_t* yr = y + (int64_t)row * plan->kpad_total + plan->koff[b];
+#pragma unroll
+    for (int i = 0; i < kNormMaxPerLane; ++i) {
+        const int j = lane + 64 * i;
+        if (j < kp) yr[j] = j < fd ? (half_t)(v[i] * inv * g[j] * scale) : (half_t)0.0f;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped GEMM over bands.
+// ---------------------------------------------------------------------------
+constexpr int kSplit = 0, kHidden = 1, kGlu = 2;
+constexpr int kBM = 128, kBN = 128, kBK = 32, kStages = 3;
+constexpr int kGemmThreads = 256;
+
+struct BandGemmArgs {
+    const BandPlan* plan;
+    const half_t* a;  // A buffer
+    int a_bytes;
+    int lda;          // elements between A rows
+    int a_band;       // elements between bands' A blocks (kSplit: unused, koff)
+    int K;            // kHidden / kGlu: K of every band
+    int layer;        // MLP layer index (weights mask_w[b * L + layer])
+    int M;            // token rows
+    void* out;
+    int ldo;
+    int o_band;       // kHidden: elements between bands' output blocks
+    int tiles_m;
+};
+
+// Tile t -> (band, tm, tn) and the band's N.
+template <int MODE>
+__device__ __forceinline__ int find_band(const BandGemmArgs& a, int t, int& b, int& tm, int& tn) {
+    const BandPlan* p = a.plan;
+    const int nb = p->nb;
+    int n;
+    if constexpr (MODE == kGlu) {
+        int start = 0;
+        b = -1;
+        for (int g = 0; g < nb; ++g) {
+            const int ng = 2 * p->fd[g];
+            const int cnt = a.tiles_m * ((ng + kBN - 1) / kBN);
+            if (t < start + cnt) {
+                b = g;
+                n = ng;
+                t -= start;
+                break;
+            }
+            start += cnt;
+        }
+        if (b < 0) return 0;
+    } else {
+        n = MODE == kSplit ? p->dim : p->hid;
+        const int per = a.tiles_m * ((n + kBN - 1) / kBN);
+        b = t / per;
+        if (b >= nb) return 0;
+        t -= b * per;
+    }
+    const int tiles_n = (n + kBN - 1) / kBN;
+    tm = t / tiles_n;
+    tn = t % tiles_n;
+    return n;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kGemmThreads, 3) void band_gemm_kernel(BandGemmArgs args) {
+    constexpr int CPR = kBK / 8;           // 16-byte chunks per LDS row (4)
+    constexpr int RPD = 64 / CPR;          // rows per 1 KB DMA instruction (16)
+    constexpr int KK = kBK / 16;           // MFMA k-substeps per k-tile
+    constexpr int WM = kBM / 2, WN = kBN / 2;
+    constexpr int MI = WM / 32, NI = WN / 32;
+    constexpr int A_INST = kBM / RPD / 4, B_INST = kBN / RPD / 4;  // per wave
+    constexpr int INST = A_INST + B_INST;
+    constexpr int STAGE = (kBM + kBN) * kBK;
+    __shared__ __attribute__((aligned(16))) half_t lds[kStages][STAGE];
+
+    int b, tm, tn;
+    const int N = find_band<MODE>(args, blockIdx.x, b, tm, tn);
+    if (N == 0) return;
+    const BandPlan* plan = args.plan;
+    const int M = args.M;
+    const int m0 = tm * kBM, n0 = tn * kBN;
+
+    // Band operands.
+    int K, a_off;
+    const half_t* W;
+    const float* bias;
+    int glu_d = 0;
+    if constexpr (MODE == kSplit) {
+        K = plan->kpad[b];
+        a_off = plan->koff[b];
+        W = packed_w(plan) + (int64_t)plan->dim * plan->koff[b];
+        bias = plan->split_b[b];
+    } else {
+        K = args.K;
+        a_off = b * args.a_band;
+        W = plan->mask_w[b * plan->L + args.layer];
+        bias = plan->mask_b[b * plan->L + args.layer];
+        if constexpr (MODE == kGlu) glu_d = plan->fd[b];
+    }
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int wm = wid >> 1, wn = wid & 1;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int sub_row = lane / CPR;
+    const int w_bytes = N * K * 2;
+
+    uint32_t aoff[A_INST], boff[B_INST];
+#pragma unroll
+    for (int i = 0; i < A_INST; ++i) {
+        const int rl = (wid * A_INST + i) * RPD + sub_row;
+        const int lchunk = (lane % CPR) ^ ((rl >> 2) & 3);
+        const int r = min(m0 + rl, M - 1);
+        aoff[i] = (uint32_t)((int64_t)a_off + (int64_t)r * args.lda + lchunk * 8) * 2u;
+    }
+#pragma unroll
+    for (int i = 0; i < B_INST; ++i) {
+        const int rl = (wid * B_INST + i) * RPD + sub_row;
+        const int lchunk = (lane % CPR) ^ ((rl >> 2) & 3);
+        int r = min(n0 + rl, N - 1);
+        if constexpr (MODE == kGlu) r = (r >> 1) + (r & 1) * glu_d;  // interleave GLU pairs
+        boff[i] = (uint32_t)(r * K + lchunk * 8) * 2u;
+    }
+    auto issue = [&](int k0, int buf) {
+        const uint32_t kb = (uint32_t)k0 * 2u;
+#pragma unroll
+        for (int i = 0; i < A_INST; ++i)
+            dma16(args.a, args.a_bytes, lds[buf] + (wid * A_INST + i) * 512, aoff[i] + kb);
+#pragma unroll
+        for (int i = 0; i < B_INST; ++i)
+            dma16(W, w_bytes, lds[buf] + kBM * kBK + (wid * B_INST + i) * 512, boff[i] + kb);
+    };
+
+    f16x acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = f16x{};
+
+    const int KT = K / kBK;
+#pragma unroll
+    for (int st = 0; st < kStages - 1; ++st) issue(min(st, KT - 1) * kBK, st);
+    for (int kt = 0; kt < KT; ++kt) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kStages - 2) * INST) : "memory");
+        lds_barrier();
+        // Refill the slot read at kt - 1 (past the end: re-fetch the last
+        // k-tile into a slot nothing reads again, keeping counts uniform).
+        issue(min(kt + kStages - 1, KT - 1) * kBK, (kt + kStages - 1) % kStages);
+        const half_t* As = lds[kt % kStages];
+        const half_t* Bs = As + kBM * kBK;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            const int c = kk * 2 + lhalf;
+            h8 af[MI], bf[NI];
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int r = wm * WM + i * 32 + lrow;
+                af[i] = *reinterpret_cast<const h8*>(As + r * kBK + ((c ^ ((r >> 2) & 3)) << 3));
+            }
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                const int r = wn * WN + j * 32 + lrow;
+                bf[j] = *reinterpret_cast<const h8*>(Bs + r * kBK + ((c ^ ((r >> 2) & 3)) << 3));
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j) acc[i][j] = mfma32x32x16(bf[j], af[i], acc[i][j]);
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+
+    // Epilogue: acc[i][j] = W_j . A_i^T, so register 4 g + e of lane l is row
+    // l % 32, column 8 g + 4 (l / 32) + e of block (i, j).  Each 32-row
+    // fragment row goes through the wave's LDS region (rows padded by 4
+    // floats) and is read back as 4 consecutive columns per lane.
+    constexpr int LDW = WN + 4;
+    constexpr int LPR = WN / 4;      // lanes per row (16)
+    constexpr int RPI = 64 / LPR;    // rows per read (4)
+    float* wl = reinterpret_cast<float*>(&lds[0][0]) + wid * (32 * LDW);
+    static_assert(4 * 32 * LDW * 4 <= (int)sizeof(lds), "epilogue staging does not fit");
+    const int rr = lane / LPR, cq = lane % LPR;
+    const int col = n0 + wn * WN + cq * 4;  // first of the lane's 4 columns
+    f4 bv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        int c = min(col + e, N - 1);
+        if constexpr (MODE == kGlu) c = (c >> 1) + (c & 1) * glu_d;
+        bv[e] = bias[c];
+    }
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<f4*>(wl + lrow * LDW + j * 32 + 8 * g + 4 * lhalf) =
+                    f4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                       acc[i][j][4 * g + 3]};
+#pragma unroll
+        for (int it = 0; it < 32 / RPI; ++it) {
+            const int lr = it * RPI + rr;
+            const int grow = m0 + wm * WM + i * 32 + lr;
+            const f4 v = *reinterpret_cast<const f4*>(wl + lr * LDW + cq * 4) + bv;
+            if (grow < M && col < N) {
+                if constexpr (MODE == kSplit) {
+                    // N = dim is a multiple of 4: the 4 columns are valid together.
+                    float* o = reinterpret_cast<float*>(args.out) + (int64_t)grow * args.ldo +
+                               b * plan->dim + col;
+                    *reinterpret_cast<f4*>(o) = v;
+                } else if constexpr (MODE == kHidden) {
+                    half_t* o = reinterpret_cast<half_t*>(args.out) + (int64_t)b * args.o_band +
+                                (int64_t)grow * args.ldo + col;
+                    *reinterpret_cast<h4*>(o) = h4{(half_t)tanhf(v[0]), (half_t)tanhf(v[1]),
+                                                   (half_t)tanhf(v[2]), (half_t)tanhf(v[3])};
+                } else {
+                    // Columns (col, col + 1) and (col + 2, col + 3) are GLU
+                    // pairs m = col / 2, col / 2 + 1 (N = 2 d is even and col
+                    // is a multiple of 4, so a lane's pairs are whole).
+                    float* o = reinterpret_cast<float*>(args.out) + (int64_t)grow * args.ldo +
+                               plan->foff[b] + (col >> 1);
+                    const float g0 = v[0] * (1.0f / (1.0f + expf(-v[1])));
+                    if (col + 2 < N) {
+                        const float g1 = v[2] * (1.0f / (1.0f + expf(-v[3])));
+                        *reinterpret_cast<float2*>(o) = float2{g0, g1};
+                    } else {
+                        o[0] = g0;
+                    }
+                }
+            }
+        }
+    }
+}
+
+int gemm_tiles_split(const BandPlan& h, int tiles_m) {
+    return h.nb * tiles_m * ((h.dim + kBN - 1) / kBN);
+}
+
+}  // namespace
+}  // namespace msst
+
+using namespace msst;
+
+namespace {
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return MSST_OK;
+    return set_error(MSST_ERR_LAUNCH, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Host mirror of the plan header, validated against the config.
+int fill_plan(const msst_band_config* c, BandPlan& h) {
+    MSST_REQUIRE(c, MSST_ERR_INVALID_ARG, "null config");
+    MSST_REQUIRE(c->num_bands >= 1 && c->num_bands <= kMaxBands && c->band_dims,
+                 MSST_ERR_UNSUPPORTED, "1..64 bands");
+    MSST_REQUIRE(c->dim >= 64 && c->dim % 64 == 0, MSST_ERR_UNSUPPORTED,
+                 "dim must be a multiple of 64");
+    MSST_REQUIRE(c->mlp_linears >= 1 && c->mlp_linears <= kMaxLinears, MSST_ERR_UNSUPPORTED,
+                 "1..8 mask-estimator linears");
+    MSST_REQUIRE(c->mlp_linears == 1 || (c->hidden >= 64 && c->hidden % 64 == 0),
+                 MSST_ERR_UNSUPPORTED, "hidden width must be a multiple of 64");
+    memset(&h, 0, sizeof(h));
+    h.nb = c->num_bands;
+    h.dim = c->dim;
+    h.hid = c->mlp_linears > 1 ? c->hidden : 0;
+    h.L = c->mlp_linears;
+    int f = 0, k = 0;
+    for (int b = 0; b < h.nb; ++b) {
+        const int d = c->band_dims[b];
+        MSST_REQUIRE(d >= 2 && d <= 1024 && d % 2 == 0, MSST_ERR_UNSUPPORTED,
+                     "band dims must be even and in [2, 1024]");
+        h.fd[b] = d;
+        h.foff[b] = f;
+        h.kpad[b] = (d + 63) / 64 * 64;
+        h.koff[b] = k;
+        f += d;
+        k += h.kpad[b];
+    }
+    h.ftot = f;
+    h.kpad_total = k;
+    return MSST_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t msst_band_plan_bytes(const msst_band_config* c) {
+    BandPlan h;
+    if (fill_plan(c, h) != MSST_OK) return -1;
+    return kPlanHeader + (int64_t)h.dim * h.kpad_total * 2;
+}
+
+extern "C" int msst_band_plan_init(const msst_band_config* c, const float* const* split_gamma,
+                                   const void* const* split_w, const float* const* split_b,
+                                   const void* const* mask_w, const float* const* mask_b,
+                                   void* plan, int64_t plan_bytes, void* stream) {
+    BandPlan h;
+    int rc = fill_plan(c, h);
+    if (rc != MSST_OK) return rc;
+    MSST_REQUIRE(plan && aligned(plan, 256), MSST_ERR_ALIGNMENT, "plan must be 256-byte aligned");
+    MSST_REQUIRE(plan_bytes >= msst_band_plan_bytes(c), MSST_ERR_WORKSPACE, "plan too small");
+    h.has_split = split_w != nullptr;
+    h.has_mask = mask_w != nullptr;
+    MSST_REQUIRE(!h.has_split || (split_gamma && split_b), MSST_ERR_INVALID_ARG,
+                 "band split needs gamma, W and bias per band");
+    MSST_REQUIRE(!h.has_mask || mask_b, MSST_ERR_INVALID_ARG, "mask estimator needs biases");
+    for (int b = 0; b < h.nb; ++b) {
+        if (h.has_split) {
+            MSST_REQUIRE(split_gamma[b] && split_w[b] && split_b[b], MSST_ERR_INVALID_ARG,
+                         "null band-split tensor");
+            h.split_gamma[b] = split_gamma[b];
+            h.split_w[b] = reinterpret_cast<const half_t*>(split_w[b]);
+            h.split_b[b] = split_b[b];
+        }
+        if (h.has_mask)
+            for (int l = 0; l < h.L; ++l) {
+                const int i = b * h.L + l;
+                MSST_REQUIRE(mask_w[i] && mask_b[i] && aligned(mask_w[i], 16),
+                             MSST_ERR_ALIGNMENT, "mask weights must be non-null, 16-byte aligned");
+                h.mask_w[i] = reinterpret_cast<const half_t*>(mask_w[i]);
+                h.mask_b[i] = mask_b[i];
+            }
+    }
+    hipStream_t s = as_stream(stream);
+    // The header is copied from host memory before the call returns
+    // (synchronous with respect to the host), then the packing kernel runs.
+    rc = hip_status(hipMemcpy(plan, &h, sizeof(h), hipMemcpyHostToDevice), "plan upload");
+    if (rc != MSST_OK) return rc;
+    if (h.has_split) {
+        const int64_t total = (int64_t)h.dim * h.kpad_total;
+        hipLaunchKernelGGL(band_pack_kernel, dim3(1024), dim3(256), 0, s,
+                           reinterpret_cast<BandPlan*>(plan), h.nb, h.dim, total);
+        rc = check_launch("band_pack_kernel");
+        if (rc != MSST_OK) return rc;
+        return hip_status(hipStreamSynchronize(s), "band_pack_kernel");
+    }
+    return MSST_OK;
+}
+
+extern "C" int64_t msst_band_split_workspace(const msst_band_config* c, int64_t rows) {
+    BandPlan h;
+    if (fill_plan(c, h) != MSST_OK || rows < 0) return -1;
+    return (rows * h.kpad_total * 2 + 255) / 256 * 256;
+}
+
+extern "C" int msst_band_split(const msst_band_config* c, const void* plan, const float* x,
+                               int64_t rows, float* out, void* workspace, int64_t ws_bytes,
+                               void* stream) {
+    BandPlan h;
+    int rc = fill_plan(c, h);
+    if (rc != MSST_OK) return rc;
+    MSST_REQUIRE(plan && x && out && workspace, MSST_ERR_INVALID_ARG, "null pointer");
+    MSST_REQUIRE(rows >= 0 && rows < (1 << 24), MSST_ERR_UNSUPPORTED, "rows out of range");
+    MSST_REQUIRE(ws_bytes >= msst_band_split_workspace(c, rows), MSST_ERR_WORKSPACE,
+                 "workspace too small");
+    MSST_REQUIRE(rows * h.kpad_total * 2 < ((int64_t)1 << 31), MSST_ERR_UNSUPPORTED,
+                 "normalised input exceeds 2^31 bytes");
+    MSST_REQUIRE(aligned(out, 16) && aligned(workspace, 16), MSST_ERR_ALIGNMENT,
+                 "out / workspace must be 16-byte aligned");
+    if (rows == 0) return MSST_OK;
+    hipStream_t s = as_stream(stream);
+    const BandPlan* p = reinterpret_cast<const BandPlan*>(plan);
+    half_t* y = reinterpret_cast<half_t*>(workspace);
+    const int64_t waves = rows * h.nb;
+    hipLaunchKernelGGL(band_norm_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p, x,
+                       (int)rows, y);
+    rc = check_launch("band_norm_kernel");
+    if (rc != MSST_OK) return rc;
+    BandGemmArgs a{};
+    a.plan = p;
+    a.a = y;
+    a.a_bytes = (int)(rows * h.kpad_total * 2);
+    a.lda = h.kpad_total;
+    a.M = (int)rows;
+    a.out = out;
+    a.ldo = h.nb * h.dim;
+    a.tiles_m = (int)((rows + kBM - 1) / kBM);
+    const int tiles = gemm_tiles_split(h, a.tiles_m);
+    hipLaunchKernelGGL(band_gemm_kernel<kSplit>, dim3((unsigned)tiles), dim3(kGemmThreads), 0, s,
+                       a);
+    return check_launch("band_gemm_kernel<split>");
+}
+
+extern "C" int64_t msst_mask_estimator_workspace(const msst_band_config* c, int64_t rows) {
+    BandPlan h;
+    if (fill_plan(c, h) != MSST_OK || rows < 0) return -1;
+    const int64_t xh = (rows * h.nb * h.dim * 2 + 255) / 256 * 256;
+    const int64_t hb = (rows * h.nb * (int64_t)h.hid * 2 + 255) / 256 * 256;
+    return xh + (h.L > 2 ? 2 : h.L > 1 ? 1 : 0) * hb;
+}
+
+extern "C" int msst_mask_estimator(const msst_band_config* c, const void* plan, const void* x,
+                                   int x_dtype, int64_t rows, float* out, void* workspace,
+                                   int64_t ws_bytes, void* stream) {
+    BandPlan h;
+    int rc = fill_plan(c, h);
+    if (rc != MSST_OK) return rc;
+    MSST_REQUIRE(plan && x && out && workspace, MSST_ERR_INVALID_ARG, "null pointer");
+    MSST_REQUIRE(x_dtype == MSST_F32 || x_dtype == MSST_F16, MSST_ERR_INVALID_ARG, "bad dtype");
+    MSST_REQUIRE(rows >= 0 && rows < (1 << 24), MSST_ERR_UNSUPPORTED, "rows out of range");
+    MSST_REQUIRE(ws_bytes >= msst_mask_estimator_workspace(c, rows), MSST_ERR_WORKSPACE,
+                 "workspace too small");
+    MSST_REQUIRE(rows * h.nb * (int64_t)std::max(h.dim, h.hid) * 2 < ((int64_t)1 << 31),
+                 MSST_ERR_UNSUPPORTED, "activations exceed 2^31 bytes");
+    MSST_REQUIRE(aligned(x, 16) && aligned(out, 8) && aligned(workspace, 256), MSST_ERR_ALIGNMENT,
+                 "x 16-byte, out 8-byte, workspace 256-byte aligned");
+    if (rows == 0) return MSST_OK;
+    hipStream_t s = as_stream(stream);
+    const BandPlan* p = reinterpret_cast<const BandPlan*>(plan);
+    char* ws = reinterpret_cast<char*>(workspace);
+    const int64_t xh_bytes = (rows * h.nb * h.dim * 2 + 255) / 256 * 256;
+    const int64_t hb_bytes = (rows * h.nb * (int64_t)h.hid * 2 + 255) / 256 * 256;
+    const half_t* xh = reinterpret_cast<const half_t*>(x);
+    if (x_dtype == MSST_F32) {
+        // ops::linear casts its fp32 input to fp16 (ops_linear.cu:155).
+        rc = msst_cast(x, MSST_F32, ws, MSST_F16, rows * h.nb * h.dim, stream);
+        if (rc != MSST_OK) return rc;
+        xh = reinterpret_cast<const half_t*>(ws);
+    }
+    half_t* hbuf[2] = {reinterpret_cast<half_t*>(ws + xh_bytes),
+                       reinterpret_cast<half_t*>(ws + xh_bytes + hb_bytes)};
+    const int tiles_m = (int)((rows + kBM - 1) / kBM);
+    const half_t* a_cur = xh;
+    int lda = h.nb * h.dim, a_band = h.dim, K = h.dim;
+    int64_t a_bytes = rows * h.nb * h.dim * 2;
+    for (int l = 0; l < h.L; ++l) {
+        BandGemmArgs a{};
+        a.plan = p;
+        a.a = a_cur;
+        a.a_bytes = (int)a_bytes;
+        a.lda = lda;
+        a.a_band = a_band;
+        a.K = K;
+        a.layer = l;
+        a.M = (int)rows;
+        a.tiles_m = tiles_m;
+        if (l < h.L - 1) {
+            // Hidden layer: tanh(A . W^T + b) -> [band][row][hid] fp16.
+            half_t* o = hbuf[l & 1];
+            a.out = o;
+            a.ldo = h.hid;
+            a.o_band = (int)(rows * h.hid);
+            const int tiles = h.nb * tiles_m * ((h.hid + kBN - 1) / kBN);
+            hipLaunchKernelGGL(band_gemm_kernel<kHidden>, dim3((unsigned)tiles),
+                               dim3(kGemmThreads), 0, s, a);
+            rc = check_launch("band_gemm_kernel<hidden>");
+            if (rc != MSST_OK) return rc;
+            a_cur = o;
+            lda = h.hid;
+            a_band = (int)(rows * h.hid);
+            K = h.hid;
+            a_bytes = rows * h.nb * (int64_t)h.hid * 2;
+        } else {
+            // Output layer + GLU -> out [row][ftot] fp32.
+            a.out = out;
+            a.ldo = h.ftot;
+            int tiles = 0;
+            for (int b = 0; b < h.nb; ++b) tiles += tiles_m * ((2 * h.fd[b] + kBN - 1) / kBN);
+            hipLaunchKernelGGL(band_gemm_kernel<kGlu>, dim3((unsigned)tiles), dim3(kGemmThreads),
+                               0, s, a);
+            rc = check_launch("band_gemm_kernel<glu>");
+            if (rc != MSST_OK) return rc;
+        }
+    }
+    return MSST_OK;
+}

@@ -20,6 +20,14 @@
  *   msst_linear_rope            ops.h:66 + :99-100 fused (linear_no_bias of
  *                               to_qkv, then apply_rotary_emb on q and k,
  *                               model_bs_roformer.cu:249, :262)
+ *   msst_band_split             model_bs_roformer.cu:337-368,
+ *                               model_mel_band_roformer.cu:658-690 (per-band
+ *                               rms_norm + linear + stack, one grouped launch)
+ *   msst_mask_estimator         model_bs_roformer.cu:374-414,
+ *                               model_mel_band_roformer.cu:696-738 (per-band
+ *                               linear/tanh MLP + glu + cat, ops.h:36, :116)
+ *   msst_band_plan_init         the per-band weight tables of
+ *                               model_bs_roformer.h:65-70, :105-115
  *   msst_rms_norm               ops.h:56               (ops_norm.cu:455-491)
  *   msst_rms_norm_gate          ops.h:56 + :134 fused  (rms_norm followed by
  *                               linear_sigmoid, model_bs_roformer.cu:243, :268)
@@ -224,6 +232,56 @@ int msst_roformer_transformer(float* x, const msst_stack_desc* desc,
                               const msst_layer_weights* w, int axis,
                               void* workspace, int64_t workspace_bytes,
                               void* stream);
+
+/* ---- Band split and mask estimator (grouped over bands) -----------------
+ * Bands: band b owns band_dims[b] consecutive features (2 * frequencies *
+ * audio channels) of the [rows, sum(band_dims)] STFT feature row.  The
+ * per-band weights stay in the caller's tensors; msst_band_plan_init copies
+ * their addresses into `plan` (device memory of msst_band_plan_bytes) once
+ * per model and packs the band-split weights into zero-padded rows.  A plan
+ * holds the band split and/or one stem's mask estimator (pass NULL for the
+ * part it does not hold).  fp16 weights (W), fp32 gamma / bias. */
+typedef struct msst_band_config {
+    int num_bands;         /* 1..64                                           */
+    const int* band_dims;  /* host array [num_bands]: even, 2..1024           */
+    int dim;               /* model dim (multiple of 64)                      */
+    int hidden;            /* mask-estimator hidden width (multiple of 64)    */
+    int mlp_linears;       /* linears per band MLP (BSRoformer: mask_estimator_depth,
+                              MelBandRoformer: mask_estimator_depth + 1); 1..8 */
+} msst_band_config;
+
+int64_t msst_band_plan_bytes(const msst_band_config* c);
+
+/* split_gamma[b] f32 [band_dims[b]], split_w[b] f16 [dim, band_dims[b]],
+ * split_b[b] f32 [dim]; mask_w[b * L + l] f16 [N_l, K_l] (K_0 = dim, N_l =
+ * hidden below the last layer, N_{L-1} = 2 band_dims[b]), mask_b likewise.
+ * Pointer arrays are host arrays of device pointers.  Synchronous: returns
+ * after the plan is written.  plan 256-byte aligned. */
+int msst_band_plan_init(const msst_band_config* c, const float* const* split_gamma,
+                        const void* const* split_w, const float* const* split_b,
+                        const void* const* mask_w, const float* const* mask_b,
+                        void* plan, int64_t plan_bytes, void* stream);
+
+/* out[r, b, :] = rms_norm(x[r, band b], gamma_b, sqrt(band_dims[b])) . W_b^T
+ * + bias_b.  x f32 [rows, sum(band_dims)], out f32 [rows, num_bands, dim]
+ * (the reference's stack along dim 2).  The normalised bands are rounded to
+ * fp16, as ops::linear casts its input.  Workspace: msst_band_split_workspace
+ * bytes, 16-byte aligned. */
+int64_t msst_band_split_workspace(const msst_band_config* c, int64_t rows);
+int msst_band_split(const msst_band_config* c, const void* plan, const float* x,
+                    int64_t rows, float* out, void* workspace, int64_t ws_bytes,
+                    void* stream);
+
+/* One stem's mask estimator: for every band b, the MLP (tanh between
+ * linears) on x[:, b, :] followed by glu; out f32 [rows, sum(band_dims)]
+ * with band b at its feature offset (the reference's cat).  x f32 or f16
+ * [rows, num_bands, dim] (fp32 input is cast to fp16 as ops::linear does);
+ * hidden activations are kept in fp16.  Workspace:
+ * msst_mask_estimator_workspace bytes, 256-byte aligned. */
+int64_t msst_mask_estimator_workspace(const msst_band_config* c, int64_t rows);
+int msst_mask_estimator(const msst_band_config* c, const void* plan, const void* x,
+                        int x_dtype, int64_t rows, float* out, void* workspace,
+                        int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -36,6 +36,8 @@ static inline float act_apply(float v, int act) {
         return 1.0f / (1.0f + expf(-v));
     case ORC_ACT_SILU:
         return v / (1.0f + expf(-v));
+    case ORC_ACT_TANH:
+        return tanhf(v);
     default:
         return v;
     }
@@ -326,4 +328,70 @@ void orc_roformer_stack(float* x, int64_t B, int64_t T, int64_t F, int64_t dim,
         memcpy(x, tmp, (size_t)(B * T * F * dim) * sizeof(float));
     }
     free(tmp); free(tcos); free(tsin); free(fcos); free(fsin);
+}
+
+/* ops_elementwise.cu:321-344: first * 1 / (1 + exp(-second)). */
+void orc_glu(const float* x, float* out, int64_t rows, int64_t n) {
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t j = 0; j < n; ++j) {
+            const float a = x[r * 2 * n + j], g = x[r * 2 * n + n + j];
+            out[r * n + j] = a * (1.0f / (1.0f + expf(-g)));
+        }
+}
+
+/* model_bs_roformer.cu:337-368: split, per-band rms_norm with scale
+ * sqrt(dims[b]), ops::linear, stack along dim 2. */
+void orc_band_split(const float* x, int64_t rows, const int* dims, int nb,
+                    const float* gamma, const float* w, const float* bias,
+                    float* out, int64_t dim) {
+    int64_t ftot = 0;
+    for (int b = 0; b < nb; ++b) ftot += dims[b];
+    int64_t off = 0;
+    for (int b = 0; b < nb; ++b) {
+        const int64_t d = dims[b];
+        float* xb = (float*)malloc((size_t)(rows * d) * sizeof(float));
+        float* ob = (float*)malloc((size_t)(rows * dim) * sizeof(float));
+        for (int64_t r = 0; r < rows; ++r) memcpy(xb + r * d, x + r * ftot + off, (size_t)d * sizeof(float));
+        orc_rms_norm(xb, gamma + off, sqrtf((float)d), xb, rows, d);
+        orc_linear(xb, w + dim * off, bias + (int64_t)b * dim, NULL, ob, rows, d, dim, ORC_ACT_NONE);
+        for (int64_t r = 0; r < rows; ++r)
+            memcpy(out + (r * nb + b) * dim, ob + r * dim, (size_t)dim * sizeof(float));
+        free(xb);
+        free(ob);
+        off += d;
+    }
+}
+
+/* model_bs_roformer.cu:374-414: per band, linear -> tanh -> ... -> linear,
+ * then glu(-1), concatenated along the last dimension. */
+void orc_mask_estimator(const float* x, int64_t rows, const int* dims, int nb,
+                        int64_t dim, int64_t hid, int L, const float* w,
+                        const float* bias, float* out) {
+    int64_t ftot = 0;
+    for (int b = 0; b < nb; ++b) ftot += dims[b];
+    int64_t off = 0, woff = 0, boff = 0;
+    for (int b = 0; b < nb; ++b) {
+        const int64_t d = dims[b];
+        float* h = (float*)malloc((size_t)(rows * dim) * sizeof(float));
+        for (int64_t r = 0; r < rows; ++r) memcpy(h + r * dim, x + (r * nb + b) * dim, (size_t)dim * sizeof(float));
+        int64_t K = dim;
+        for (int l = 0; l < L; ++l) {
+            const int64_t N = (l == L - 1) ? 2 * d : hid;
+            float* o = (float*)malloc((size_t)(rows * N) * sizeof(float));
+            orc_linear(h, w + woff, bias + boff, NULL, o, rows, K, N,
+                       l < L - 1 ? ORC_ACT_TANH : ORC_ACT_NONE);
+            woff += N * K;
+            boff += N;
+            free(h);
+            h = o;
+            K = N;
+        }
+        float* g = (float*)malloc((size_t)(rows * d) * sizeof(float));
+        orc_glu(h, g, rows, d);
+        for (int64_t r = 0; r < rows; ++r) memcpy(out + r * ftot + off, g + r * d, (size_t)d * sizeof(float));
+        free(g);
+        free(h);
+        off += d;
+    }
 }

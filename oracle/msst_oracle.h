@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-enum { ORC_ACT_NONE = 0, ORC_ACT_GELU = 1, ORC_ACT_SIGMOID = 2, ORC_ACT_SILU = 3 };
+enum { ORC_ACT_NONE = 0, ORC_ACT_GELU = 1, ORC_ACT_SIGMOID = 2, ORC_ACT_SILU = 3, ORC_ACT_TANH = 4 };
 
 /* Weights of one transformer (attention + feed-forward) as the two Roformer
  * models hold them (model_bs_roformer.h:78-98). final_gamma is the
@@ -51,7 +51,7 @@ void orc_linear(const float* x, const float* w, const float* b,
                 const float* residual, float* out,
                 int64_t M, int64_t K, int64_t N, int act);
 
-/* Elementwise activations (ops_fused.cu:21-32). */
+/* Elementwise activations (ops_fused.cu:21-32; tanh: ops_elementwise.cu:84-88). */
 void orc_activation(const float* x, float* out, int64_t n, int act);
 
 /* y = x * rsqrt(sum(x^2) + 1e-12) * gamma * scale per row
@@ -100,6 +100,30 @@ void orc_roformer_stack(float* x, int64_t B, int64_t T, int64_t F, int64_t dim,
                         int64_t H, int64_t Dh, int64_t ff, int64_t depth,
                         const orc_layer_weights* layers,
                         const float* final_gamma);
+
+/* GLU over the last dimension: out[r, j] = x[r, j] * sigmoid(x[r, j + n]) for
+ * x [rows, 2n] (ops_elementwise.cu:321-388). */
+void orc_glu(const float* x, float* out, int64_t rows, int64_t n);
+
+/* Band split (model_bs_roformer.cu:337-368; model_mel_band_roformer.cu:658-690).
+ * x [rows, sum(dims)]: band b is columns [off_b, off_b + dims[b]).  For each
+ * band: y = rms_norm(x_b, gamma_b, sqrt(dims[b])), out[r, b, :] = y . W_b^T +
+ * bias_b.  gamma: the gamma_b concatenated [sum(dims)]; w: the W_b [dim,
+ * dims[b]] concatenated (band b at dim * off_b); bias [nb, dim];
+ * out [rows, nb, dim]. */
+void orc_band_split(const float* x, int64_t rows, const int* dims, int nb,
+                    const float* gamma, const float* w, const float* bias,
+                    float* out, int64_t dim);
+
+/* Mask estimator of one stem (model_bs_roformer.cu:374-414;
+ * model_mel_band_roformer.cu:696-738).  x [rows, nb, dim].  Per band b: an
+ * MLP of L linears, tanh between them (not after the last), widths dim ->
+ * hid -> ... -> hid -> 2 dims[b], then GLU; the result fills columns
+ * [off_b, off_b + dims[b]) of out [rows, sum(dims)].  w / bias hold the
+ * layers in (band, layer) order, each W [N_l, K_l] row-major. */
+void orc_mask_estimator(const float* x, int64_t rows, const int* dims, int nb,
+                        int64_t dim, int64_t hid, int L, const float* w,
+                        const float* bias, float* out);
 
 #ifdef __cplusplus
 }

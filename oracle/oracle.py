@@ -19,7 +19,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "_build", "libmsst_oracle.so")
 
-ACT = {"none": 0, "gelu": 1, "sigmoid": 2, "silu": 3}
+ACT = {"none": 0, "gelu": 1, "sigmoid": 2, "silu": 3, "tanh": 4}
 
 _lib = None
 
@@ -65,6 +65,11 @@ def _declare(l: ctypes.CDLL) -> None:
                                   ctypes.POINTER(LayerWeightsC), _fp, _fp]
     l.orc_roformer_stack.argtypes = [_fp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                      _i64, ctypes.POINTER(LayerWeightsC), _fp]
+    _ip = ctypes.POINTER(ctypes.c_int)
+    l.orc_glu.argtypes = [_fp, _fp, _i64, _i64]
+    l.orc_band_split.argtypes = [_fp, _i64, _ip, ctypes.c_int, _fp, _fp, _fp, _fp, _i64]
+    l.orc_mask_estimator.argtypes = [_fp, _i64, _ip, ctypes.c_int, _i64, _i64, ctypes.c_int,
+                                     _fp, _fp, _fp]
 
 
 def _f32(a) -> np.ndarray:
@@ -205,3 +210,48 @@ def roformer_stack(x, layers, heads: int, dim_head: int, final_gamma=None) -> np
     lib().orc_roformer_stack(_p(x), B, T, F, dim, heads, dim_head, ff, len(layers) // 2,
                              arr, _p(fg))
     return x
+
+
+def glu(x) -> np.ndarray:
+    """x [..., 2n] -> x[..., :n] * sigmoid(x[..., n:])."""
+    x = _f32(x)
+    n = x.shape[-1] // 2
+    out = np.empty(x.shape[:-1] + (n,), np.float32)
+    lib().orc_glu(_p(x), _p(out), x.size // (2 * n), n)
+    return out
+
+
+def _dims(dims):
+    d = np.ascontiguousarray(dims, dtype=np.int32)
+    return d, d.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+
+
+def band_split(x, dims, gammas, ws, biases) -> np.ndarray:
+    """x [rows, sum(dims)]; per band b: gammas[b] [dims[b]], ws[b] [dim, dims[b]],
+    biases[b] [dim].  Returns [rows, nb, dim]."""
+    x = _f32(x)
+    rows = x.shape[0]
+    nb = len(dims)
+    dim = ws[0].shape[0]
+    g = _f32(np.concatenate([np.ravel(a) for a in gammas]))
+    w = _f32(np.concatenate([np.ravel(a) for a in ws]))
+    b = _f32(np.concatenate([np.ravel(a) for a in biases]))
+    d, dp = _dims(dims)
+    out = np.empty((rows, nb, dim), np.float32)
+    lib().orc_band_split(_p(x), rows, dp, nb, _p(g), _p(w), _p(b), _p(out), dim)
+    return out
+
+
+def mask_estimator(x, dims, ws, biases) -> np.ndarray:
+    """x [rows, nb, dim]; ws[b][l] / biases[b][l]: the L linears of band b's
+    MLP (tanh between, GLU after).  Returns [rows, sum(dims)]."""
+    x = _f32(x)
+    rows, nb, dim = x.shape
+    L = len(ws[0])
+    hid = ws[0][0].shape[0] if L > 1 else 0
+    w = _f32(np.concatenate([np.ravel(a) for band in ws for a in band]))
+    b = _f32(np.concatenate([np.ravel(a) for band in biases for a in band]))
+    d, dp = _dims(dims)
+    out = np.empty((rows, int(d.sum())), np.float32)
+    lib().orc_mask_estimator(_p(x), rows, dp, nb, dim, hid, L, _p(w), _p(b), _p(out))
+    return out

@@ -132,3 +132,45 @@ def test_product_does_not_reference_oracle():
                 text = open(os.path.join(dirpath, f), errors="ignore").read().lower()
                 for needle in ("msst_oracle", "import oracle", "from oracle", "orc_"):
                     assert needle not in text, (f, needle)
+
+
+def _band_cfg(msst, dims, dim=64, hidden=128, L=2):
+    arr = (ctypes.c_int * len(dims))(*dims)
+    return msst.BandConfig(len(dims), arr, dim, hidden, L), arr
+
+
+def test_band_config_validation(msst):
+    lib = msst.lib()
+    cfg, _keep = _band_cfg(msst, [4, 8, 130])
+    # header 256-aligned + dim * sum(ceil64(dims)) halves
+    n = lib.msst_band_plan_bytes(ctypes.byref(cfg))
+    assert n > 0 and n % 2 == 0 and n >= 64 * (64 + 64 + 192) * 2
+    assert lib.msst_band_split_workspace(ctypes.byref(cfg), 10) >= 10 * 320 * 2
+    for dims, dim, hid, L in (([3], 64, 128, 2),          # odd band dim
+                              ([2] * 65, 64, 128, 2),     # too many bands
+                              ([4], 60, 128, 2),          # dim not a multiple of 64
+                              ([4], 64, 100, 2),          # hidden not a multiple of 64
+                              ([4], 64, 128, 9),          # too many linears
+                              ([2048], 64, 128, 2)):      # band wider than 1024
+        cfg, _k = _band_cfg(msst, dims, dim, hid, L)
+        assert lib.msst_band_plan_bytes(ctypes.byref(cfg)) == -1
+        rc = lib.msst_band_split(ctypes.byref(cfg), ctypes.c_void_p(256), ctypes.c_void_p(256), 4,
+                                 ctypes.c_void_p(256), ctypes.c_void_p(256), 1 << 20, None)
+        assert rc == UNSUPPORTED, _last(msst)
+
+
+def test_band_calls_reject_before_launch(msst):
+    lib = msst.lib()
+    cfg, _keep = _band_cfg(msst, [4, 8])
+    p = ctypes.c_void_p(4096)
+    assert lib.msst_band_split(ctypes.byref(cfg), None, p, 4, p, p, 1 << 20, None) == INVALID
+    assert lib.msst_band_split(ctypes.byref(cfg), p, p, 4, p, p, 8, None) == WORKSPACE
+    assert lib.msst_mask_estimator(ctypes.byref(cfg), p, p, 7, 4, p, p, 1 << 20, None) == INVALID
+    assert lib.msst_mask_estimator(ctypes.byref(cfg), p, p, 0, 4, p, p, 8, None) == WORKSPACE
+    assert lib.msst_mask_estimator(ctypes.byref(cfg), p, ctypes.c_void_p(4098), 0, 4, p, p,
+                                   1 << 20, None) == ALIGN
+    # plan init: misaligned plan, too-small plan (no device memory is touched)
+    assert lib.msst_band_plan_init(ctypes.byref(cfg), None, None, None, None, None,
+                                   ctypes.c_void_p(4100), 1 << 20, None) == ALIGN
+    assert lib.msst_band_plan_init(ctypes.byref(cfg), None, None, None, None, None,
+                                   p, 16, None) == WORKSPACE

@@ -210,3 +210,116 @@ def test_stack_axis_order_matters(oracle):
     a = oracle.roformer_stack(x, [oracle.LayerWeights(**w) for w in layers], H, Dh)
     b = oracle.roformer_stack(x, [oracle.LayerWeights(**w) for w in layers[::-1]], H, Dh)
     assert rel_err(a, b) > 1e-3
+
+
+# ------------------------------------------------ band split / mask estimator
+BSR_FREQS = [2] * 24 + [4] * 12 + [12] * 8 + [24] * 8 + [48] * 8 + [128, 129]
+
+
+def test_tanh_and_glu_closed_forms(oracle):
+    x = np.linspace(-20, 20, 4001, dtype=np.float32)
+    t = oracle.activation(x, "tanh")
+    np.testing.assert_allclose(t, np.tanh(x.astype(np.float64)), rtol=2e-7, atol=1e-7)
+    assert t[2000] == 0.0 and np.all(t[:-1] <= t[1:]) and np.array_equal(t, -t[::-1])
+    a = rnd(9, 5)
+    # zero gate -> half of the value; large gate -> the value; order of halves
+    np.testing.assert_array_equal(oracle.glu(np.concatenate([a, np.zeros_like(a)], 1)), a * 0.5)
+    np.testing.assert_allclose(oracle.glu(np.concatenate([a, np.full_like(a, 40.0)], 1)), a,
+                               rtol=1e-7)
+    g = rnd(9, 5)
+    r = a.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))
+    assert rel_err(oracle.glu(np.concatenate([a, g], 1)), r) < 1e-6
+
+
+def _split_weights(dims, dim, seed=3):
+    rng = np.random.default_rng(seed)
+    gam = [(1.0 + 0.02 * rng.standard_normal(d)).astype(np.float32) for d in dims]
+    ws = [(0.02 * rng.standard_normal((dim, d))).astype(np.float32) for d in dims]
+    bs = [(0.02 * rng.standard_normal(dim)).astype(np.float32) for d in dims]
+    return gam, ws, bs
+
+
+def test_band_split_single_band_is_norm_then_linear(oracle):
+    dims, dim = [24], 16
+    x = rnd(11, 24)
+    g, w, b = _split_weights(dims, dim)
+    y = oracle.band_split(x, dims, g, w, b)
+    r = oracle.linear(oracle.rms_norm(x, g[0], math.sqrt(24)), w[0], b[0])
+    np.testing.assert_array_equal(y[:, 0, :], r)
+
+
+def test_band_split_band_independence_and_scale_invariance(oracle):
+    dims, dim = [4, 8, 12, 6], 32
+    off = np.concatenate([[0], np.cumsum(dims)])
+    x = rnd(7, sum(dims))
+    g, w, b = _split_weights(dims, dim)
+    y = oracle.band_split(x, dims, g, w, b)
+    for bi in range(len(dims)):
+        x2 = x.copy()
+        x2[:, off[bi]:off[bi + 1]] *= 3.5           # rms_norm is scale invariant
+        x3 = x.copy()
+        x3[:, off[bi]:off[bi + 1]] = rnd(7, dims[bi])  # only band bi changes
+        y2 = oracle.band_split(x2, dims, g, w, b)
+        y3 = oracle.band_split(x3, dims, g, w, b)
+        assert rel_err(y2, y) < 1e-6
+        others = [j for j in range(len(dims)) if j != bi]
+        np.testing.assert_array_equal(y3[:, others], y[:, others])
+        assert not np.allclose(y3[:, bi], y[:, bi])
+    # each band equals the single-band split of its own slice
+    for bi in range(len(dims)):
+        yi = oracle.band_split(x[:, off[bi]:off[bi + 1]], [dims[bi]], [g[bi]], [w[bi]], [b[bi]])
+        np.testing.assert_array_equal(yi[:, 0], y[:, bi])
+
+
+def _mask_weights(dims, dim, hid, L, seed=4):
+    rng = np.random.default_rng(seed)
+    ws, bs = [], []
+    for d in dims:
+        wl, bl, K = [], [], dim
+        for l in range(L):
+            N = 2 * d if l == L - 1 else hid
+            wl.append((rng.standard_normal((N, K)) / math.sqrt(K)).astype(np.float32))
+            bl.append((0.02 * rng.standard_normal(N)).astype(np.float32))
+            K = N
+        ws.append(wl)
+        bs.append(bl)
+    return ws, bs
+
+
+@pytest.mark.parametrize("L", [1, 2, 3])
+def test_mask_estimator_is_per_band_mlp_then_glu(oracle, L):
+    dims, dim, hid = [4, 10, 6], 16, 24
+    x = rnd(9, len(dims), dim)
+    ws, bs = _mask_weights(dims, dim, hid, L)
+    y = oracle.mask_estimator(x, dims, ws, bs)
+    off = np.concatenate([[0], np.cumsum(dims)])
+    for bi, d in enumerate(dims):
+        h = x[:, bi]
+        for l in range(L):
+            h = oracle.linear(h, ws[bi][l], bs[bi][l], "tanh" if l < L - 1 else "none")
+        np.testing.assert_array_equal(y[:, off[bi]:off[bi + 1]], oracle.glu(h))
+    # float64 restatement of the same network from numpy primitives
+    for bi, d in enumerate(dims):
+        h = x[:, bi].astype(np.float64)
+        for l in range(L):
+            h = h @ ws[bi][l].T.astype(np.float64) + bs[bi][l]
+            if l < L - 1:
+                h = np.tanh(h)
+        r = h[:, :d] / (1.0 + np.exp(-h[:, d:]))
+        assert rel_err(y[:, off[bi]:off[bi + 1]], r) < 1e-5
+
+
+def test_mask_estimator_gate_half_selects(oracle):
+    """W rows of the gate half set to zero and bias 0 -> sigmoid(0) = 1/2, so
+    the mask is half of the value half: a transposed or swapped GLU half fails."""
+    dims, dim = [6, 4], 8
+    x = rnd(5, 2, dim)
+    ws, bs = _mask_weights(dims, dim, 0, 1)
+    for bi, d in enumerate(dims):
+        ws[bi][0][d:] = 0.0
+        bs[bi][0][d:] = 0.0
+    y = oracle.mask_estimator(x, dims, ws, bs)
+    off = [0, 6, 10]
+    for bi, d in enumerate(dims):
+        v = oracle.linear(x[:, bi], ws[bi][0][:d], bs[bi][0][:d])
+        np.testing.assert_allclose(y[:, off[bi]:off[bi + 1]], 0.5 * v, rtol=1e-6, atol=1e-7)
