@@ -91,6 +91,8 @@ _SIGS = {
     "msst_roformer_stack_workspace": ([ctypes.POINTER(StackDesc)], _i64),
     "msst_roformer_stack": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights), _vp,
                              _vp, _i64, _vp], _int),
+    "msst_tanh": ([_vp, _vp, _int, _i64, _vp], _int),
+    "msst_glu": ([_vp, _vp, _int, _i64, _i64, _vp], _int),
     "msst_band_plan_bytes": ([_BCP], _i64),
     "msst_band_plan_init": ([_BCP, _PP, _PP, _PP, _PP, _PP, _vp, _i64, _vp], _int),
     "msst_band_split_workspace": ([_BCP, _i64], _i64),
@@ -343,6 +345,24 @@ class RoformerStack:
             _ptr(self.workspace), self.workspace.numel(), _stream()),
             "msst_roformer_transformer")
         return x
+
+
+def tanh(x, out=None):
+    import torch
+    if out is None:
+        out = torch.empty_like(x)
+    check(lib().msst_tanh(_ptr(x), _ptr(out), _dt(x), x.numel(), _stream()), "msst_tanh")
+    return out
+
+
+def glu(x):
+    """Last-axis GLU: x[..., :n] * sigmoid(x[..., n:])."""
+    import torch
+    half = x.shape[-1] // 2
+    out = torch.empty(*x.shape[:-1], half, dtype=x.dtype, device=x.device)
+    check(lib().msst_glu(_ptr(x), _ptr(out), _dt(x), x.numel() // (2 * half), half, _stream()),
+          "msst_glu")
+    return out
 
 
 class BandPlan:

@@ -6,6 +6,9 @@
 //                          (model_mel_band_roformer.cu:76-115, :142-163)
 //   msst_cast              f32 <-> f16 (tensor.cu:1269-1294)
 //   msst_add               elementwise add (tensor.cu:1365-1447)
+//   msst_tanh              elementwise tanh (ops_elementwise.cu:84-88, :138)
+//   msst_glu               last-axis GLU, first half * sigmoid(second half)
+//                          (ops_elementwise.cu:321-388)
 //   msst_swap_axes12       [A,P,Q,R] -> [A,Q,P,R], the permute({0,2,1,3})
 //                          .contiguous() of the depth loop
 //                          (model_bs_roformer.cu:491, :509; tensor.cu:868-903)
@@ -63,6 +66,27 @@ __global__ __launch_bounds__(256) void add_kernel(const T* a, const T* b, T* out
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (; i < n; i += stride) out[i] = (T)((float)a[i] + (float)b[i]);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void tanh_kernel(const T* x, T* out, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) out[i] = (T)tanhf((float)x[i]);
+}
+
+// out[r, j] = x[r, j] * 1 / (1 + exp(-x[r, j + half])), x [rows, 2 half].
+template <typename T>
+__global__ __launch_bounds__(256) void glu_kernel(const T* __restrict__ x, T* __restrict__ out,
+                                                  int64_t rows, int64_t half) {
+    const int64_t n = rows * half;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        const int64_t r = i / half, j = i - r * half;
+        const float a = (float)x[r * 2 * half + j], g = (float)x[r * 2 * half + half + j];
+        out[i] = (T)(a * (1.0f / (1.0f + expf(-g))));
+    }
 }
 
 // [A,P,Q,R] -> [A,Q,P,R]; one thread per 16-byte (or element) chunk of R.
@@ -178,6 +202,42 @@ extern "C" int msst_add(const void* a, const void* b, void* out, int dtype, int6
                            reinterpret_cast<const float*>(a), reinterpret_cast<const float*>(b),
                            reinterpret_cast<float*>(out), n);
     return check_launch("add_kernel");
+}
+
+extern "C" int msst_tanh(const void* x, void* out, int dtype, int64_t n, void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(x && out, MSST_ERR_INVALID_ARG, "null tensor pointer");
+    MSST_REQUIRE(is_dtype(dtype), MSST_ERR_INVALID_ARG, "bad dtype");
+    MSST_REQUIRE(n >= 0, MSST_ERR_INVALID_ARG, "negative size");
+    if (n == 0) return MSST_OK;
+    hipStream_t s = as_stream(stream);
+    if (dtype == MSST_F16)
+        hipLaunchKernelGGL(tanh_kernel<half_t>, dim3(grid_for(n)), dim3(256), 0, s,
+                           reinterpret_cast<const half_t*>(x), reinterpret_cast<half_t*>(out), n);
+    else
+        hipLaunchKernelGGL(tanh_kernel<float>, dim3(grid_for(n)), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(x), reinterpret_cast<float*>(out), n);
+    return check_launch("tanh_kernel");
+}
+
+extern "C" int msst_glu(const void* x, void* out, int dtype, int64_t rows, int64_t half,
+                        void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(x && out && x != out, MSST_ERR_INVALID_ARG, "null or aliased tensor pointer");
+    MSST_REQUIRE(is_dtype(dtype), MSST_ERR_INVALID_ARG, "bad dtype");
+    MSST_REQUIRE(rows >= 0 && half >= 0, MSST_ERR_INVALID_ARG, "negative size");
+    if (rows * half == 0) return MSST_OK;
+    hipStream_t s = as_stream(stream);
+    const unsigned grid = grid_for(rows * half);
+    if (dtype == MSST_F16)
+        hipLaunchKernelGGL(glu_kernel<half_t>, dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const half_t*>(x), reinterpret_cast<half_t*>(out),
+                           rows, half);
+    else
+        hipLaunchKernelGGL(glu_kernel<float>, dim3(grid), dim3(256), 0, s,
+                           reinterpret_cast<const float*>(x), reinterpret_cast<float*>(out), rows,
+                           half);
+    return check_launch("glu_kernel");
 }
 
 extern "C" int msst_swap_axes12(const void* src, void* dst, int dtype, int64_t A, int64_t P,

@@ -2,6 +2,7 @@
 // rules; each function cites the reference function it stands in for.
 #include "ops.h"
 
+#include <algorithm>
 #include <cmath>
 #include <string>
 
@@ -97,6 +98,32 @@ Tensor rms_norm(const Tensor& x, const Tensor& gamma, float scale) {
         check(msst_rms_norm(x.data_ptr(), abi(x.dtype()), g.data_f32(), scale, out.data_ptr(),
                             abi(x.dtype()), rows, D, stream()),
               "rms_norm");
+    return out;
+}
+
+// ops_elementwise.cu:84-88, :138
+Tensor tanh_act(const Tensor& x) {
+    Tensor out = Tensor::empty(x.shape(), x.dtype());
+    if (x.numel() > 0)
+        check(msst_tanh(x.data_ptr(), out.data_ptr(), abi(x.dtype()), x.numel(), stream()),
+              "tanh_act");
+    return out;
+}
+
+// ops_elementwise.cu:345-388 (last dimension)
+Tensor glu(const Tensor& x, int dim) {
+    const int nd = x.ndim();
+    if (nd < 1 || (dim != -1 && dim != nd - 1))
+        throw std::runtime_error("glu: only the last dimension is supported");
+    const int64_t full = x.size(-1);
+    if (full % 2 != 0) throw std::runtime_error("glu: last dimension must be even");
+    std::vector<int64_t> shape = x.shape();
+    shape.back() = full / 2;
+    Tensor out = Tensor::empty(shape, x.dtype());
+    const int64_t rows = full > 0 ? x.numel() / full : 0;
+    if (rows > 0 && full > 0)
+        check(msst_glu(x.data_ptr(), out.data_ptr(), abi(x.dtype()), rows, full / 2, stream()),
+              "glu");
     return out;
 }
 
@@ -212,6 +239,122 @@ void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int hea
     Tensor work = Tensor::empty({ws}, DType::Float16);  // byte buffer (>= ws bytes)
     check(msst_roformer_stack(x.data_f32(), &d, lw.data(), fg, work.data_ptr(), 2 * ws, stream()),
           "roformer_stack");
+}
+
+// ---------------------------------------------------------------------------
+// BandPlan
+// ---------------------------------------------------------------------------
+msst_band_config BandPlan::config() const {
+    msst_band_config c;
+    c.num_bands = (int)dims_.size();
+    c.band_dims = dims_.data();
+    c.dim = dim_;
+    c.hidden = hidden_;
+    c.mlp_linears = linears_;
+    return c;
+}
+
+BandPlan::BandPlan(std::vector<int> band_dims, int dim, const BandSplitWeights* split,
+                   const MaskEstimatorWeights* mask)
+    : dims_(std::move(band_dims)), dim_(dim) {
+    const size_t nb = dims_.size();
+    if (mask) {
+        if (mask->w.size() != nb || mask->b.size() != nb || mask->w[0].empty())
+            throw std::runtime_error("BandPlan: mask estimator needs weights for every band");
+        linears_ = (int)mask->w[0].size();
+        hidden_ = linears_ > 1 ? (int)mask->w[0][0].size(0) : 0;
+    }
+    const msst_band_config c = config();
+    const int64_t bytes = msst_band_plan_bytes(&c);
+    if (bytes < 0) throw std::runtime_error("BandPlan: unsupported band configuration");
+    plan_ = Tensor::empty({(bytes + 3) / 4}, DType::Float32);
+    auto f32v = [&](const Tensor& t) -> const float* {
+        if (t.dtype() == DType::Float32) return t.data_f32();
+        keep_.push_back(t.to_f32());
+        return keep_.back().data_f32();
+    };
+    auto f16w = [&](const Tensor& t) -> const void* {
+        if (t.dtype() != DType::Float16)
+            throw std::runtime_error("BandPlan: band weights must be fp16 (g_quantize_fp16)");
+        return t.data_ptr();
+    };
+    std::vector<const float*> sg, sb, mb;
+    std::vector<const void*> sw, mw;
+    if (split) {
+        if (split->gamma.size() != nb || split->w.size() != nb || split->b.size() != nb)
+            throw std::runtime_error("BandPlan: band split needs weights for every band");
+        for (size_t b = 0; b < nb; ++b) {
+            if (split->w[b].ndim() != 2 || split->w[b].size(0) != dim ||
+                split->w[b].size(1) != dims_[b] || split->gamma[b].numel() != dims_[b] ||
+                split->b[b].numel() != dim)
+                throw std::runtime_error("BandPlan: band split weight " + std::to_string(b) +
+                                         " has the wrong shape");
+            sg.push_back(f32v(split->gamma[b]));
+            sw.push_back(f16w(split->w[b]));
+            sb.push_back(f32v(split->b[b]));
+        }
+    }
+    if (mask) {
+        for (size_t b = 0; b < nb; ++b) {
+            if ((int)mask->w[b].size() != linears_ || (int)mask->b[b].size() != linears_)
+                throw std::runtime_error("BandPlan: every band MLP needs the same depth");
+            int64_t K = dim;
+            for (int l = 0; l < linears_; ++l) {
+                const int64_t N = l == linears_ - 1 ? 2 * dims_[b] : hidden_;
+                const Tensor& w = mask->w[b][l];
+                if (w.ndim() != 2 || w.size(0) != N || w.size(1) != K ||
+                    mask->b[b][l].numel() != N)
+                    throw std::runtime_error("BandPlan: mask estimator weight (" +
+                                             std::to_string(b) + ", " + std::to_string(l) +
+                                             ") has the wrong shape");
+                mw.push_back(f16w(w));
+                mb.push_back(f32v(mask->b[b][l]));
+                K = N;
+            }
+        }
+    }
+    check(msst_band_plan_init(&c, split ? sg.data() : nullptr, split ? sw.data() : nullptr,
+                              split ? sb.data() : nullptr, mask ? mw.data() : nullptr,
+                              mask ? mb.data() : nullptr, plan_.data_ptr(), bytes, stream()),
+          "BandPlan");
+}
+
+Tensor BandPlan::band_split(const Tensor& x) const {
+    int64_t ftot = 0;
+    for (int d : dims_) ftot += d;
+    if (x.ndim() < 1 || x.size(-1) != ftot || x.dtype() != DType::Float32)
+        throw std::runtime_error("band_split: x must be fp32 [..., sum(band_dims)]");
+    const int64_t rows = x.numel() / ftot;
+    std::vector<int64_t> shape = x.shape();
+    shape.back() = (int64_t)dims_.size();
+    shape.push_back(dim_);
+    Tensor out = Tensor::empty(shape, DType::Float32);
+    const msst_band_config c = config();
+    const int64_t wsb = msst_band_split_workspace(&c, rows);
+    Tensor ws = Tensor::empty({std::max<int64_t>((wsb + 3) / 4, 1)}, DType::Float32);
+    check(msst_band_split(&c, plan_.data_ptr(), x.data_f32(), rows, out.data_f32(), ws.data_ptr(),
+                          wsb, stream()),
+          "band_split");
+    return out;
+}
+
+Tensor BandPlan::mask_estimator(const Tensor& x) const {
+    const int64_t nb = (int64_t)dims_.size();
+    if (x.ndim() < 2 || x.size(-1) != dim_ || x.size(-2) != nb)
+        throw std::runtime_error("mask_estimator: x must be [..., num_bands, dim]");
+    int64_t ftot = 0;
+    for (int d : dims_) ftot += d;
+    const int64_t rows = x.numel() / (nb * dim_);
+    std::vector<int64_t> shape(x.shape().begin(), x.shape().end() - 2);
+    shape.push_back(ftot);
+    Tensor out = Tensor::empty(shape, DType::Float32);
+    const msst_band_config c = config();
+    const int64_t wsb = msst_mask_estimator_workspace(&c, rows);
+    Tensor ws = Tensor::empty({std::max<int64_t>((wsb + 3) / 4, 1)}, DType::Float32);
+    check(msst_mask_estimator(&c, plan_.data_ptr(), x.data_ptr(), abi(x.dtype()), rows,
+                              out.data_f32(), ws.data_ptr(), wsb, stream()),
+          "mask_estimator");
+    return out;
 }
 
 }  // namespace ops

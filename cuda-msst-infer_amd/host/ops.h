@@ -27,6 +27,7 @@
 
 #include <vector>
 
+#include "msst_hip.h"
 #include "tensor.h"
 
 namespace cudasep {
@@ -69,6 +70,11 @@ Tensor scaled_dot_product_attention(const Tensor& q, const Tensor& k, const Tens
 // q,k: [B, H, N, D] rotated in place (interleaved pairs); cos/sin [N, D/2].
 void apply_rotary_emb(Tensor& q, Tensor& k, const Tensor& cos_freqs, const Tensor& sin_freqs);
 
+// ops_elementwise.cu:84-88, :138 (tanhf) and :321-388 (first * sigmoid(second));
+// glu splits the last dimension only (the Roformers' use, dim = -1).
+Tensor tanh_act(const Tensor& x);
+Tensor glu(const Tensor& x, int dim = -1);
+
 Tensor linear_gelu(const Tensor& x, const Tensor& weight, const Tensor& bias);
 Tensor linear_silu(const Tensor& x, const Tensor& weight, const Tensor& bias);
 Tensor linear_sigmoid(const Tensor& x, const Tensor& weight, const Tensor& bias);
@@ -92,6 +98,41 @@ struct RoformerLayer {
 // output norm) may be empty.  Matrices must all be fp16 or all fp32.
 void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int heads,
                     int dim_head, const Tensor& final_gamma);
+
+// ---- Band split and mask estimator (model_bs_roformer.cu:337-414,
+// model_mel_band_roformer.cu:658-738) as grouped launches over all bands.
+// band_dims[b] = 2 * freqs_in_band * audio_channels (the reference's
+// band_freq_dims_).  Weights per band as the models hold them
+// (model_bs_roformer.h:65-70, :105-115): gamma [fd] and W [dim, fd], b [dim]
+// for the split; w[b][l] / bias[b][l] for the L linears of band b's MLP.
+// Matrices must be fp16 (the reference's fp16 mode converts them at load,
+// weights.cu:510-524); gammas and biases may be fp16 or fp32.
+struct BandSplitWeights {
+    std::vector<Tensor> gamma, w, b;
+};
+struct MaskEstimatorWeights {
+    std::vector<std::vector<Tensor>> w, b;  // [band][layer]
+};
+
+class BandPlan {
+public:
+    // Either weight set may be null.  The tensors must outlive the plan.
+    BandPlan(std::vector<int> band_dims, int dim, const BandSplitWeights* split,
+             const MaskEstimatorWeights* mask);
+    // x [..., sum(band_dims)] fp32 -> [..., num_bands, dim] fp32
+    // (apply_band_split: split, rms_norm * sqrt(fd), linear, stack).
+    Tensor band_split(const Tensor& x) const;
+    // x [..., num_bands, dim] -> [..., sum(band_dims)] fp32
+    // (apply_mask_estimator: per-band MLP with tanh, glu, cat).
+    Tensor mask_estimator(const Tensor& x) const;
+
+private:
+    std::vector<int> dims_;
+    int dim_ = 0, hidden_ = 0, linears_ = 1;
+    Tensor plan_;
+    std::vector<Tensor> keep_;  // fp32 copies of fp16 gammas / biases
+    msst_band_config config() const;
+};
 
 }  // namespace ops
 }  // namespace cudasep

@@ -41,6 +41,8 @@
  *   msst_cast                   tensor.cu:1269-1294 (to_dtype)
  *   msst_add                    tensor.cu:1365-1447 (operator+, add_)
  *   msst_swap_axes12            tensor.cu:868-903 (permute + contiguous)
+ *   msst_tanh                   ops.h:36 tanh_act      (ops_elementwise.cu:84-88, :138)
+ *   msst_glu                    ops.h:116 glu(x, -1)   (ops_elementwise.cu:321-388)
  *   msst_roformer_stack         model_bs_roformer.cu:482-539,
  *                               model_mel_band_roformer.cu:843-906
  *   msst_roformer_transformer   model_bs_roformer.cu:310-331,
@@ -179,6 +181,13 @@ int msst_cast(const void* src, int src_dtype, void* dst, int dst_dtype,
 /* out[i] = a[i] + b[i] (all of one dtype; out may alias a or b). */
 int msst_add(const void* a, const void* b, void* out, int dtype, int64_t n,
              void* stream);
+
+/* out = tanh(x), elementwise (in place allowed). */
+int msst_tanh(const void* x, void* out, int dtype, int64_t n, void* stream);
+
+/* GLU over the last axis: out[r, j] = x[r, j] * sigmoid(x[r, j + half]),
+ * x [rows, 2 * half], out [rows, half] (not aliased). */
+int msst_glu(const void* x, void* out, int dtype, int64_t rows, int64_t half, void* stream);
 
 /* dst[A,Q,P,R] = src[A,P,Q,R]: the permute({0,2,1,3}).contiguous() of the
  * depth loop (model_bs_roformer.cu:491, :509).  src and dst must differ. */

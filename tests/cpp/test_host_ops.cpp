@@ -256,6 +256,78 @@ static void test_tensor() {
     expect(ok, "operator+ is exact");
 }
 
+static void test_bands() {
+    // tanh_act / glu (ops.h:36, :116)
+    const int64_t R = 37, H2 = 26;
+    auto x = randn(R * 2 * H2, 2.0f, 41);
+    std::vector<float> rt(x.size()), rg(R * H2);
+    orc_activation(x.data(), rt.data(), (int64_t)x.size(), ORC_ACT_TANH);
+    orc_glu(x.data(), rg.data(), R, H2);
+    Tensor xd = dev(x, {R, 2 * H2}, DType::Float32);
+    check_close("tanh_act f32", ops::tanh_act(xd), rt, 1e-6);
+    Tensor g = ops::glu(xd, -1);
+    expect(g.shape() == std::vector<int64_t>({R, H2}), "glu halves the last dim");
+    check_close("glu f32", g, rg, 1e-6);
+    expect_throw("glu on an odd last dim", [&] { ops::glu(xd.reshape({-1, 13}), -1); });
+
+    // BandPlan: 5 bands of a stereo split, dim 64, MLP of 2 linears (hidden 128).
+    const std::vector<int> dims = {4, 8, 16, 48, 516};
+    const int nb = (int)dims.size(), dim = 64, hid = 128, L = 2;
+    int ftot = 0;
+    for (int d : dims) ftot += d;
+    const int64_t B = 2, T = 31, rows = B * T;
+    ops::BandSplitWeights sw;
+    ops::MaskEstimatorWeights mw;
+    std::vector<float> gcat, wcat, bcat, mwcat, mbcat;
+    for (int b = 0; b < nb; ++b) {
+        auto gam = randn(dims[b], 0.02f, 100 + b, 1.0f);
+        auto w = round16(randn((size_t)dim * dims[b], 1.0f / std::sqrt((float)dims[b]), 200 + b));
+        auto bb = randn(dim, 0.02f, 300 + b);
+        sw.gamma.push_back(dev(gam, {dims[b]}, DType::Float32));
+        sw.w.push_back(dev(w, {dim, dims[b]}, DType::Float16));
+        sw.b.push_back(dev(bb, {dim}, DType::Float32));
+        gcat.insert(gcat.end(), gam.begin(), gam.end());
+        wcat.insert(wcat.end(), w.begin(), w.end());
+        bcat.insert(bcat.end(), bb.begin(), bb.end());
+        std::vector<Tensor> wl, bl;
+        int K = dim;
+        for (int l = 0; l < L; ++l) {
+            const int N = l == L - 1 ? 2 * dims[b] : hid;
+            auto ww = round16(randn((size_t)N * K, 1.0f / std::sqrt((float)K), 400 + 10 * b + l));
+            auto wb = randn(N, 0.02f, 500 + 10 * b + l);
+            wl.push_back(dev(ww, {N, K}, DType::Float16));
+            bl.push_back(dev(wb, {N}, DType::Float16));  // fp16 bias is promoted
+            mwcat.insert(mwcat.end(), ww.begin(), ww.end());
+            auto wb16 = round16(wb);
+            mbcat.insert(mbcat.end(), wb16.begin(), wb16.end());
+            K = N;
+        }
+        mw.w.push_back(wl);
+        mw.b.push_back(bl);
+    }
+    ops::BandPlan plan(dims, dim, &sw, &mw);
+    auto xin = randn((size_t)rows * ftot, 1.0f, 77);
+    Tensor feats = plan.band_split(dev(xin, {B, T, ftot}, DType::Float32));
+    expect(feats.shape() == std::vector<int64_t>({B, T, nb, dim}), "band_split -> [B, T, nb, dim]");
+    std::vector<float> rf((size_t)rows * nb * dim), rm((size_t)rows * ftot);
+    orc_band_split(xin.data(), rows, dims.data(), nb, gcat.data(), wcat.data(), bcat.data(),
+                   rf.data(), dim);
+    check_close("band_split", feats, rf, 2e-2);
+    Tensor m = plan.mask_estimator(feats);
+    expect(m.shape() == std::vector<int64_t>({B, T, ftot}), "mask_estimator -> [B, T, sum dims]");
+    const std::vector<float> fh = feats.to_cpu_f32();
+    orc_mask_estimator(fh.data(), rows, dims.data(), nb, dim, hid, L, mwcat.data(), mbcat.data(),
+                       rm.data());
+    check_close("mask_estimator", m, rm, 2e-2);
+    expect_throw("BandPlan with an fp32 matrix", [&] {
+        ops::BandSplitWeights bad = sw;
+        bad.w[0] = bad.w[0].to_f32();
+        ops::BandPlan p(dims, dim, &bad, nullptr);
+    });
+    expect_throw("mask_estimator on the wrong band count",
+                 [&] { plan.mask_estimator(Tensor::zeros({rows, nb + 1, dim})); });
+}
+
 int main() {
     try {
         test_tensor();
@@ -263,6 +335,7 @@ int main() {
         test_rms_norm();
         test_rope_attention();
         test_stack();
+        test_bands();
         cudasep::CudaContext::instance().sync();
     } catch (const std::exception& ex) {
         std::printf("FAIL: uncaught exception: %s\n", ex.what());

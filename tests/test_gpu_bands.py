@@ -122,3 +122,18 @@ def test_band_plan_holds_both_parts_and_is_reusable(msst, oracle, cuda):
         rf = oracle.band_split(x, dims, g, w, b)
         rm = oracle.mask_estimator(rf, dims, ws, bs)
         assert per_band_err(m, rm, dims) < TOL_F16
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_tanh_and_glu(msst, oracle, cuda, dt):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((333, 2 * 129)) * 3).astype(np.float32)
+    tdt = torch.float32 if dt == "f32" else torch.float16
+    if dt == "f16":
+        x = r16(x)
+    tol = 1e-6 if dt == "f32" else 1e-3
+    t = host(msst.tanh(dev(x, tdt)))
+    assert rel_err(t, oracle.activation(x, "tanh")) < tol
+    g = host(msst.glu(dev(x, tdt)))
+    assert g.shape == (333, 129)
+    assert rel_err(g, oracle.glu(x)) < tol

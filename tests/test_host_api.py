@@ -25,6 +25,10 @@ SIGNATURES = [
     "cudasep::ops::rms_norm(cudasep::Tensor const&, cudasep::Tensor const&, float)",
     "cudasep::ops::apply_rotary_emb(cudasep::Tensor&, cudasep::Tensor&, cudasep::Tensor const&, cudasep::Tensor const&)",
     "cudasep::ops::scaled_dot_product_attention(cudasep::Tensor const&, cudasep::Tensor const&, cudasep::Tensor const&, float, float)",
+    "cudasep::ops::tanh_act(cudasep::Tensor const&)",
+    "cudasep::ops::glu(cudasep::Tensor const&, int)",
+    "cudasep::ops::BandPlan::band_split(cudasep::Tensor const&) const",
+    "cudasep::ops::BandPlan::mask_estimator(cudasep::Tensor const&) const",
     "cudasep::clear_attention_graph_cache()",
     "cudasep::CudaContext::instance()",
     "cudasep::Tensor::empty(std::vector<long, std::allocator<long> >, cudasep::DType)",
