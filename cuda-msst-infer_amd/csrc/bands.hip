@@ -18,7 +18,8 @@
 //                        one group per band; the tile -> band map is a scan
 //                        over the bands' tile counts.  Epilogues:
 //                          kSplit   out[r, b, :] = acc + bias_b       (fp32)
-//                          kHidden  tanh(acc + bias)                  (fp16)
+//                          kHidden  tanh(acc + bias)                  (fp16,
+//                                   tanh_fast: msst_common.hpp)
 //                          kGlu     v[m] * sigmoid(v[m + d])          (fp32)
 //                        For kGlu the W rows are read interleaved (tile row
 //                        2m is W row m, 2m + 1 is W row m + d), so each GLU
@@ -140,6 +141,7 @@ struct BandGemmArgs {
     int ldo;
     int o_band;       // kHidden: elements between bands' output blocks
     int tiles_m;
+    int per_xcd;      // tiles per XCD (the grid is 8 * per_xcd workgroups)
 };
 
 // Tile t -> (band, tm, tn) and the band's N.
@@ -188,8 +190,13 @@ __global__ __launch_bounds__(kGemmThreads, 3) void band_gemm_kernel(BandGemmArgs
     constexpr int STAGE = (kBM + kBN) * kBK;
     __shared__ __attribute__((aligned(16))) half_t lds[kStages][STAGE];
 
+    // XCD-aware: workgroups are dealt round-robin to the 8 XCDs, so
+    // workgroup w takes tile (w % 8) * per_xcd + w / 8 and each XCD walks a
+    // contiguous run of tiles -- a few bands at a time, whose W stays in
+    // that XCD's L2.
+    const int t = (int)(blockIdx.x & 7) * args.per_xcd + (int)(blockIdx.x >> 3);
     int b, tm, tn;
-    const int N = find_band<MODE>(args, blockIdx.x, b, tm, tn);
+    const int N = find_band<MODE>(args, t, b, tm, tn);
     if (N == 0) return;
     const BandPlan* plan = args.plan;
     const int M = args.M;
@@ -326,8 +333,9 @@ __global__ __launch_bounds__(kGemmThreads, 3) void band_gemm_kernel(BandGemmArgs
                 } else if constexpr (MODE == kHidden) {
                     half_t* o = reinterpret_cast<half_t*>(args.out) + (int64_t)b * args.o_band +
                                 (int64_t)grow * args.ldo + col;
-                    *reinterpret_cast<h4*>(o) = h4{(half_t)tanhf(v[0]), (half_t)tanhf(v[1]),
-                                                   (half_t)tanhf(v[2]), (half_t)tanhf(v[3])};
+                    *reinterpret_cast<h4*>(o) =
+                        h4{(half_t)tanh_fast(v[0]), (half_t)tanh_fast(v[1]),
+                           (half_t)tanh_fast(v[2]), (half_t)tanh_fast(v[3])};
                 } else {
                     // Columns (col, col + 1) and (col + 2, col + 3) are GLU
                     // pairs m = col / 2, col / 2 + 1 (N = 2 d is even and col
@@ -490,8 +498,9 @@ extern "C" int msst_band_split(const msst_band_config* c, const void* plan, cons
     a.ldo = h.nb * h.dim;
     a.tiles_m = (int)((rows + kBM - 1) / kBM);
     const int tiles = gemm_tiles_split(h, a.tiles_m);
-    hipLaunchKernelGGL(band_gemm_kernel<kSplit>, dim3((unsigned)tiles), dim3(kGemmThreads), 0, s,
-                       a);
+    a.per_xcd = (tiles + 7) / 8;
+    hipLaunchKernelGGL(band_gemm_kernel<kSplit>, dim3((unsigned)(8 * a.per_xcd)),
+                       dim3(kGemmThreads), 0, s, a);
     return check_launch("band_gemm_kernel<split>");
 }
 
@@ -555,7 +564,8 @@ extern "C" int msst_mask_estimator(const msst_band_config* c, const void* plan, 
             a.ldo = h.hid;
             a.o_band = (int)(rows * h.hid);
             const int tiles = h.nb * tiles_m * ((h.hid + kBN - 1) / kBN);
-            hipLaunchKernelGGL(band_gemm_kernel<kHidden>, dim3((unsigned)tiles),
+            a.per_xcd = (tiles + 7) / 8;
+            hipLaunchKernelGGL(band_gemm_kernel<kHidden>, dim3((unsigned)(8 * a.per_xcd)),
                                dim3(kGemmThreads), 0, s, a);
             rc = check_launch("band_gemm_kernel<hidden>");
             if (rc != MSST_OK) return rc;
@@ -570,8 +580,9 @@ extern "C" int msst_mask_estimator(const msst_band_config* c, const void* plan, 
             a.ldo = h.ftot;
             int tiles = 0;
             for (int b = 0; b < h.nb; ++b) tiles += tiles_m * ((2 * h.fd[b] + kBN - 1) / kBN);
-            hipLaunchKernelGGL(band_gemm_kernel<kGlu>, dim3((unsigned)tiles), dim3(kGemmThreads),
-                               0, s, a);
+            a.per_xcd = (tiles + 7) / 8;
+            hipLaunchKernelGGL(band_gemm_kernel<kGlu>, dim3((unsigned)(8 * a.per_xcd)),
+                               dim3(kGemmThreads), 0, s, a);
             rc = check_launch("band_gemm_kernel<glu>");
             if (rc != MSST_OK) return rc;
         }

@@ -61,6 +61,21 @@ __global__ __launch_bounds__(256) void cast_kernel(const S* __restrict__ src, D*
     for (; i < n; i += stride) dst[i] = (D)(float)src[i];
 }
 
+// 4 elements per thread (n % 4 == 0, 16-byte aligned source).
+template <typename S, typename D>
+__global__ __launch_bounds__(256) void cast4_kernel(const S* __restrict__ src, D* __restrict__ dst,
+                                                    int64_t n4) {
+    typedef S SV __attribute__((ext_vector_type(4)));
+    typedef D DV __attribute__((ext_vector_type(4)));
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (; i < n4; i += stride) {
+        const SV v = reinterpret_cast<const SV*>(src)[i];
+        reinterpret_cast<DV*>(dst)[i] = DV{(D)(float)v[0], (D)(float)v[1], (D)(float)v[2],
+                                           (D)(float)v[3]};
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void add_kernel(const T* a, const T* b, T* out, int64_t n) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -169,6 +184,18 @@ extern "C" int msst_cast(const void* src, int src_dtype, void* dst, int dst_dtyp
     if (n == 0) return MSST_OK;
     hipStream_t s = as_stream(stream);
     const unsigned grid = grid_for(n);
+    if (n % 4 == 0 && aligned(src, 16) && aligned(dst, 16) && src_dtype != dst_dtype) {
+        const unsigned g4 = grid_for(n / 4);
+        if (src_dtype == MSST_F32)
+            hipLaunchKernelGGL((cast4_kernel<float, half_t>), dim3(g4), dim3(256), 0, s,
+                               reinterpret_cast<const float*>(src), reinterpret_cast<half_t*>(dst),
+                               n / 4);
+        else
+            hipLaunchKernelGGL((cast4_kernel<half_t, float>), dim3(g4), dim3(256), 0, s,
+                               reinterpret_cast<const half_t*>(src), reinterpret_cast<float*>(dst),
+                               n / 4);
+        return check_launch("cast4_kernel");
+    }
     if (src_dtype == MSST_F32 && dst_dtype == MSST_F16)
         hipLaunchKernelGGL((cast_kernel<float, half_t>), dim3(grid), dim3(256), 0, s,
                            reinterpret_cast<const float*>(src), reinterpret_cast<half_t*>(dst), n);
