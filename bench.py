@@ -262,6 +262,49 @@ def kernel_table(msst, torch, layers, B):
     return table
 
 
+# BSRoformer's band layout: 62 bands over 1025 STFT bins, stereo (2 * freqs
+# * 2 channels features per band); mask-estimator MLP of 2 linears, hidden
+# 4 * dim (mlp_expansion_factor 4).
+BSR_FREQS = [2] * 24 + [4] * 12 + [12] * 8 + [24] * 8 + [48] * 8 + [128, 129]
+
+
+def band_table(msst, torch, B):
+    """Band split and one stem's mask estimator on one chunk's frames
+    (rows = B * 801), HIP-event timed, 50 launches after one warm-up."""
+    dims = [4 * f for f in BSR_FREQS]
+    rows, nb, hid, ftot = B * FRAMES, len(dims), 4 * DIM, sum(dims)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+
+    def n(*s, sd=0.02, dt=torch.float16):
+        return (torch.randn(*s, device="cuda", generator=gen) * sd).to(dt)
+
+    split = ([1.0 + n(d, dt=torch.float32) for d in dims], [n(DIM, d) for d in dims],
+             [n(DIM, dt=torch.float32) for d in dims])
+    mask = ([[n(hid, DIM), n(2 * d, hid)] for d in dims],
+            [[n(hid, dt=torch.float32), n(2 * d, dt=torch.float32)] for d in dims])
+    plan = msst.BandPlan(dims, DIM, split=split, mask=mask)
+    x = torch.randn(rows, ftot, device="cuda", generator=gen)
+    feats = plan.band_split(x)
+    m = plan.mask_estimator(feats)
+    out = {}
+    f_split = 2.0 * rows * ftot * DIM
+    f_mask = 2.0 * rows * nb * DIM * hid + 2.0 * rows * hid * 2 * ftot
+    for name, fn, flops, nbytes in (
+            ("band_split", lambda: plan.band_split(x, out=feats), f_split,
+             4 * rows * ftot + 4 * rows * nb * DIM + 2 * DIM * ftot),
+            ("mask_estimator", lambda: plan.mask_estimator(feats, out=m), f_mask,
+             4 * rows * nb * DIM + 4 * rows * ftot + 2 * nb * hid * (DIM + 2 * 2 * ftot // nb))):
+        fn()
+        us = time_events(torch, fn, 50) / 50 * 1e3
+        tf = flops / (us * 1e-6) / 1e12
+        out[name] = {"us": round(us, 2), "tflops": round(tf, 1),
+                     "frac_mfma": round(tf / PEAK_F16_TFLOPS, 4),
+                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    out["config"] = f"BSRoformer bands: 62 bands, features {ftot}, rows {rows}, dim {DIM}, " \
+                    f"MLP {DIM}->{hid}->2*band, fp16 weights, fp32 input"
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -378,6 +421,9 @@ def main():
         },
     }
     out["kernels"] = kernel_table(msst, torch, layers, B)
+    # Either side of the stack (not part of the timed step): band split and
+    # one stem's mask estimator on the same chunk.
+    out["bands"] = band_table(msst, torch, B)
     if not args.no_cpu:
         cpu, parity = cpu_baseline_and_parity(msst, torch, args)
         out["cpu_baseline"] = cpu
