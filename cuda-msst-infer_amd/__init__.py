@@ -61,7 +61,8 @@ class StackDesc(ctypes.Structure):
 
 class BandConfig(ctypes.Structure):
     _fields_ = [("num_bands", _int), ("band_dims", ctypes.POINTER(_int)), ("dim", _int),
-                ("hidden", _int), ("mlp_linears", _int)]
+                ("hidden", _int), ("mlp_linears", _int), ("audio_channels", _int),
+                ("stft_bins", _int), ("freq_indices", ctypes.POINTER(_int))]
 
 
 _BCP = ctypes.POINTER(BandConfig)
@@ -99,6 +100,9 @@ _SIGS = {
     "msst_band_split": ([_BCP, _vp, _vp, _i64, _vp, _vp, _i64, _vp], _int),
     "msst_mask_estimator_workspace": ([_BCP, _i64], _i64),
     "msst_mask_estimator": ([_BCP, _vp, _vp, _int, _i64, _vp, _vp, _i64, _vp], _int),
+    "msst_band_gather": ([_BCP, _vp, _vp, _i64, _i64, _vp, _vp], _int),
+    "msst_mask_merge_workspace": ([_BCP, _i64, _i64, _i64], _i64),
+    "msst_mask_merge": ([_BCP, _vp, _vp, _i64, _vp, _i64, _i64, _int, _vp, _vp, _i64, _vp], _int),
     "msst_roformer_transformer": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights),
                                    _int, _vp, _i64, _vp], _int),
 }
@@ -371,14 +375,20 @@ class BandPlan:
     biases) per band; mask = (ws, biases) per band, each a list of the L
     linears.  Keeps references to every tensor it points at."""
 
-    def __init__(self, dims, dim, split=None, mask=None, hidden=0):
+    def __init__(self, dims, dim, split=None, mask=None, hidden=0, channels=0, stft_bins=0,
+                 freq_indices=None):
         import torch
         self.dims = [int(d) for d in dims]
         self._dims_c = (_int * len(self.dims))(*self.dims)
         L = len(mask[0][0]) if mask is not None else 1
         if mask is not None and L > 1:
             hidden = mask[0][0][0].shape[0]
-        self.cfg = BandConfig(len(self.dims), self._dims_c, int(dim), int(hidden), int(L))
+        self._fidx_c = None
+        if freq_indices is not None:
+            self._fidx_c = (_int * len(freq_indices))(*[int(v) for v in freq_indices])
+        self.channels, self.stft_bins = int(channels), int(stft_bins)
+        self.cfg = BandConfig(len(self.dims), self._dims_c, int(dim), int(hidden), int(L),
+                              self.channels, self.stft_bins, self._fidx_c)
         nbytes = lib().msst_band_plan_bytes(ctypes.byref(self.cfg))
         if nbytes < 0:
             check(-2, "msst_band_plan_bytes")
@@ -424,4 +434,26 @@ class BandPlan:
         check(lib().msst_mask_estimator(ctypes.byref(self.cfg), _ptr(self.plan), _ptr(x), _dt(x),
                                         rows, _ptr(out), _ptr(ws), wsb, _stream()),
               "msst_mask_estimator")
+        return out
+
+    def band_gather(self, stft, batch):
+        """stft f32 [batch * ch, F, T, 2] -> band features f32 [batch, T, sum(dims)]."""
+        import torch
+        T = stft.shape[2]
+        out = torch.empty(batch, T, sum(self.dims), device=stft.device)
+        check(lib().msst_band_gather(ctypes.byref(self.cfg), _ptr(self.plan), _ptr(stft), batch,
+                                     T, _ptr(out), _stream()), "msst_band_gather")
+        return out
+
+    def mask_merge(self, masks, stft, batch, zero_dc=True):
+        """masks f32 [stems, batch, T, sum(dims)], stft f32 [batch * ch, F, T, 2]
+        -> masked STFT f32 [batch * stems * ch, F, T, 2]."""
+        import torch
+        stems, T = masks.shape[0], stft.shape[2]
+        out = torch.empty(batch * stems * self.channels, self.stft_bins, T, 2, device=stft.device)
+        wsb = lib().msst_mask_merge_workspace(ctypes.byref(self.cfg), batch, stems, T)
+        ws = torch.empty(max(int(wsb), 16), dtype=torch.uint8, device=stft.device)
+        check(lib().msst_mask_merge(ctypes.byref(self.cfg), _ptr(self.plan), _ptr(masks), stems,
+                                    _ptr(stft), batch, T, int(bool(zero_dc)), _ptr(out), _ptr(ws),
+                                    wsb, _stream()), "msst_mask_merge")
         return out

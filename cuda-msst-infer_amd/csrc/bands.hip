@@ -32,6 +32,7 @@
 // the plan with scalar loads.
 #include <algorithm>
 #include <cstring>
+#include <vector>
 
 #include "msst_common.hpp"
 
@@ -55,13 +56,22 @@ struct BandPlan {
     const float* split_b[kMaxBands];
     const half_t* mask_w[kMaxBands * kMaxLinears];
     const float* mask_b[kMaxBands * kMaxLinears];
+    // STFT side: n_idx = ftot / 2 band feature pairs over nbins = F * ch
+    // interleaved bins; `identity` when pair j is bin j (no averaging).
+    int ch, F, nbins, n_idx, identity;
+    int64_t idx_off;  // byte offset of the index tables in the plan
 };
-// The packed band-split weights follow the plan header: band b is
-// [dim][kpad_b] halves at element offset dim * koff_b.
+// Plan layout: header | packed band-split weights (band b is [dim][kpad_b]
+// halves at element offset dim * koff_b) | fidx [n_idx] | csr_off [nbins + 1]
+// | csr_list [n_idx] (int32; csr lists, per bin g, the pairs j with
+// fidx[j] == g in ascending order).
 constexpr int64_t kPlanHeader = (sizeof(BandPlan) + 255) / 256 * 256;
 
 __device__ __forceinline__ const half_t* packed_w(const BandPlan* p) {
     return reinterpret_cast<const half_t*>(reinterpret_cast<const char*>(p) + kPlanHeader);
+}
+__device__ __forceinline__ const int* plan_ints(const BandPlan* p) {
+    return reinterpret_cast<const int*>(reinterpret_cast<const char*>(p) + p->idx_off);
 }
 
 // ---------------------------------------------------------------------------
@@ -355,6 +365,107 @@ __global__ __launch_bounds__(kGemmThreads, 3) void band_gemm_kernel(BandGemmArgs
     }
 }
 
+// ---------------------------------------------------------------------------
+// STFT <-> band features.  Both kernels move [.., frames, pairs] <-> [.., bins,
+// frames] through a 64 x 64 LDS tile (float2 = one complex value), so global
+// reads and writes are both contiguous along their fastest axis.
+// ---------------------------------------------------------------------------
+constexpr int kTile = 64;
+
+// out[b, t, j] = stft[b * ch + s, f, t] with f * ch + s = fidx[j].
+// Grid (frame tiles, pair tiles, batch).
+__global__ __launch_bounds__(256) void band_gather_kernel(const BandPlan* __restrict__ plan,
+                                                          const float2* __restrict__ stft,
+                                                          int T, float2* __restrict__ out) {
+    __shared__ float2 tile[kTile][kTile + 1];
+    const int tid = threadIdx.x;
+    const int t0 = blockIdx.x * kTile, j0 = blockIdx.y * kTile, b = blockIdx.z;
+    const int ch = plan->ch, F = plan->F, n = plan->n_idx;
+    const int* fidx = plan_ints(plan);
+#pragma unroll 4
+    for (int it = 0; it < kTile / 4; ++it) {
+        const int jj = it * 4 + (tid >> 6), tt = tid & 63;
+        const int j = j0 + jj, t = t0 + tt;
+        float2 v = float2{0.0f, 0.0f};
+        if (j < n && t < T) {
+            const int g = fidx[j];
+            const int f = g / ch, sc = g - f * ch;
+            v = stft[((int64_t)(b * ch + sc) * F + f) * T + t];
+        }
+        tile[jj][tt] = v;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int it = 0; it < kTile / 4; ++it) {
+        const int tt = it * 4 + (tid >> 6), jj = tid & 63;
+        const int j = j0 + jj, t = t0 + tt;
+        if (j < n && t < T) out[((int64_t)b * T + t) * n + j] = tile[jj][tt];
+    }
+}
+
+// Per mask row (stem, batch, frame): the mean over the pairs that hold each
+// bin, mg[row, g] = sum_{j in csr(g)} masks[row, j] / max(count, 1e-8)
+// (scatter_add then the clamped division).  Grid (bin blocks, rows).
+__global__ __launch_bounds__(256) void mask_mean_kernel(const BandPlan* __restrict__ plan,
+                                                        const float2* __restrict__ masks,
+                                                        float2* __restrict__ mg) {
+    const int nbins = plan->nbins, n = plan->n_idx;
+    const int g = blockIdx.x * 256 + threadIdx.x;
+    if (g >= nbins) return;
+    const int* ints = plan_ints(plan);
+    const int* off = ints + n;
+    const int* list = off + nbins + 1;
+    const int64_t row = blockIdx.y;
+    const float2* mr = masks + row * n;
+    float2 acc = float2{0.0f, 0.0f};
+    const int k0 = off[g], k1 = off[g + 1];
+    for (int k = k0; k < k1; ++k) {
+        const float2 v = mr[list[k]];
+        acc.x += v.x;
+        acc.y += v.y;
+    }
+    const float den = fmaxf((float)(k1 - k0), 1e-8f);
+    mg[row * nbins + g] = float2{acc.x / den, acc.y / den};
+}
+
+// out[(b * stems + n) * ch + s, f, t] = stft[b * ch + s, f, t] * m[n, b, t, g]
+// (complex), g = f * ch + s; bin 0 zeroed when zero_dc.  m is [stems][batch,
+// frames, nbins].  Grid (frame tiles, bin tiles, stems * batch).
+__global__ __launch_bounds__(256) void mask_apply_kernel(const BandPlan* __restrict__ plan,
+                                                         const float2* __restrict__ m,
+                                                         const float2* __restrict__ stft,
+                                                         int batch, int T, int zero_dc,
+                                                         float2* __restrict__ out) {
+    __shared__ float2 tile[kTile][kTile + 1];
+    const int tid = threadIdx.x;
+    const int t0 = blockIdx.x * kTile, g0 = blockIdx.y * kTile;
+    const int nb = blockIdx.z;  // stem-major: n * batch + b
+    const int n = nb / batch, b = nb - n * batch;
+    const int ch = plan->ch, F = plan->F, nbins = plan->nbins;
+    const int stems = gridDim.z / batch;
+    const float2* mrow = m + (int64_t)nb * T * nbins;
+#pragma unroll 4
+    for (int it = 0; it < kTile / 4; ++it) {
+        const int tt = it * 4 + (tid >> 6), gg = tid & 63;
+        const int t = t0 + tt, g = g0 + gg;
+        tile[gg][tt] = (t < T && g < nbins) ? mrow[(int64_t)t * nbins + g] : float2{0.0f, 0.0f};
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int it = 0; it < kTile / 4; ++it) {
+        const int gg = it * 4 + (tid >> 6), tt = tid & 63;
+        const int t = t0 + tt, g = g0 + gg;
+        if (t < T && g < nbins) {
+            const int f = g / ch, sc = g - f * ch;
+            const float2 x = stft[((int64_t)(b * ch + sc) * F + f) * T + t];
+            const float2 k = tile[gg][tt];
+            float2 o = float2{x.x * k.x - x.y * k.y, x.x * k.y + x.y * k.x};
+            if (zero_dc && f == 0) o = float2{0.0f, 0.0f};
+            out[((int64_t)((b * stems + n) * ch + sc) * F + f) * T + t] = o;
+        }
+    }
+}
+
 int gemm_tiles_split(const BandPlan& h, int tiles_m) {
     return h.nb * tiles_m * ((h.dim + kBN - 1) / kBN);
 }
@@ -401,7 +512,28 @@ int fill_plan(const msst_band_config* c, BandPlan& h) {
     }
     h.ftot = f;
     h.kpad_total = k;
+    h.n_idx = f / 2;
+    h.ch = c->audio_channels;
+    h.F = c->stft_bins;
+    h.identity = c->freq_indices == nullptr;
+    if (h.ch > 0 || h.F > 0) {
+        MSST_REQUIRE((h.ch == 1 || h.ch == 2) && h.F >= 1, MSST_ERR_UNSUPPORTED,
+                     "STFT side needs 1 or 2 channels and stft_bins >= 1");
+        h.nbins = h.F * h.ch;
+        if (h.identity)
+            MSST_REQUIRE(h.n_idx == h.nbins, MSST_ERR_INVALID_ARG,
+                         "without freq_indices the bands must cover every bin once");
+        else
+            for (int j = 0; j < h.n_idx; ++j)
+                MSST_REQUIRE(c->freq_indices[j] >= 0 && c->freq_indices[j] < h.nbins,
+                             MSST_ERR_INVALID_ARG, "freq_indices out of range");
+    }
+    h.idx_off = kPlanHeader + ((int64_t)h.dim * h.kpad_total * 2 + 255) / 256 * 256;
     return MSST_OK;
+}
+
+int64_t plan_bytes(const BandPlan& h) {
+    return h.idx_off + 4 * ((int64_t)h.n_idx * 2 + h.nbins + 1);
 }
 
 }  // namespace
@@ -409,7 +541,7 @@ int fill_plan(const msst_band_config* c, BandPlan& h) {
 extern "C" int64_t msst_band_plan_bytes(const msst_band_config* c) {
     BandPlan h;
     if (fill_plan(c, h) != MSST_OK) return -1;
-    return kPlanHeader + (int64_t)h.dim * h.kpad_total * 2;
+    return plan_bytes(h);
 }
 
 extern "C" int msst_band_plan_init(const msst_band_config* c, const float* const* split_gamma,
@@ -448,6 +580,22 @@ extern "C" int msst_band_plan_init(const msst_band_config* c, const float* const
     // (synchronous with respect to the host), then the packing kernel runs.
     rc = hip_status(hipMemcpy(plan, &h, sizeof(h), hipMemcpyHostToDevice), "plan upload");
     if (rc != MSST_OK) return rc;
+    if (h.nbins > 0) {
+        // fidx, then the inverse map as CSR (bins in order, pairs ascending).
+        std::vector<int> ints((size_t)h.n_idx * 2 + h.nbins + 1, 0);
+        int* fidx = ints.data();
+        int* off = fidx + h.n_idx;
+        int* list = off + h.nbins + 1;
+        for (int j = 0; j < h.n_idx; ++j) fidx[j] = h.identity ? j : c->freq_indices[j];
+        for (int j = 0; j < h.n_idx; ++j) ++off[fidx[j] + 1];
+        for (int g = 0; g < h.nbins; ++g) off[g + 1] += off[g];
+        std::vector<int> fill(off, off + h.nbins);
+        for (int j = 0; j < h.n_idx; ++j) list[fill[fidx[j]]++] = j;
+        rc = hip_status(hipMemcpy(reinterpret_cast<char*>(plan) + h.idx_off, ints.data(),
+                                  ints.size() * sizeof(int), hipMemcpyHostToDevice),
+                        "plan index upload");
+        if (rc != MSST_OK) return rc;
+    }
     if (h.has_split) {
         const int64_t total = (int64_t)h.dim * h.kpad_total;
         hipLaunchKernelGGL(band_pack_kernel, dim3(1024), dim3(256), 0, s,
@@ -588,4 +736,72 @@ extern "C" int msst_mask_estimator(const msst_band_config* c, const void* plan, 
         }
     }
     return MSST_OK;
+}
+
+extern "C" int msst_band_gather(const msst_band_config* c, const void* plan, const float* stft,
+                                int64_t batch, int64_t frames, float* out, void* stream) {
+    BandPlan h;
+    int rc = fill_plan(c, h);
+    if (rc != MSST_OK) return rc;
+    MSST_REQUIRE(h.nbins > 0, MSST_ERR_INVALID_ARG, "config has no STFT side");
+    MSST_REQUIRE(plan && stft && out, MSST_ERR_INVALID_ARG, "null pointer");
+    MSST_REQUIRE(batch >= 0 && frames >= 0 && batch < 65536 && frames < (1 << 24),
+                 MSST_ERR_UNSUPPORTED, "batch / frames out of range");
+    MSST_REQUIRE(aligned(stft, 8) && aligned(out, 8), MSST_ERR_ALIGNMENT, "8-byte alignment");
+    if (batch == 0 || frames == 0) return MSST_OK;
+    const dim3 grid((unsigned)((frames + kTile - 1) / kTile), (unsigned)((h.n_idx + kTile - 1) / kTile),
+                    (unsigned)batch);
+    hipLaunchKernelGGL(band_gather_kernel, grid, dim3(256), 0, as_stream(stream),
+                       reinterpret_cast<const BandPlan*>(plan), reinterpret_cast<const float2*>(stft),
+                       (int)frames, reinterpret_cast<float2*>(out));
+    return check_launch("band_gather_kernel");
+}
+
+extern "C" int64_t msst_mask_merge_workspace(const msst_band_config* c, int64_t batch,
+                                             int64_t stems, int64_t frames) {
+    BandPlan h;
+    if (fill_plan(c, h) != MSST_OK || batch < 0 || stems < 0 || frames < 0) return -1;
+    return h.identity ? 0 : batch * stems * frames * (int64_t)h.nbins * 8;
+}
+
+extern "C" int msst_mask_merge(const msst_band_config* c, const void* plan, const float* masks,
+                               int64_t stems, const float* stft, int64_t batch, int64_t frames,
+                               int zero_dc, float* out, void* workspace, int64_t ws_bytes,
+                               void* stream) {
+    BandPlan h;
+    int rc = fill_plan(c, h);
+    if (rc != MSST_OK) return rc;
+    MSST_REQUIRE(h.nbins > 0, MSST_ERR_INVALID_ARG, "config has no STFT side");
+    MSST_REQUIRE(plan && masks && stft && out, MSST_ERR_INVALID_ARG, "null pointer");
+    MSST_REQUIRE(batch >= 0 && stems >= 0 && frames >= 0 && batch * stems < 65536 &&
+                     frames < (1 << 24),
+                 MSST_ERR_UNSUPPORTED, "batch / stems / frames out of range");
+    MSST_REQUIRE(ws_bytes >= msst_mask_merge_workspace(c, batch, stems, frames),
+                 MSST_ERR_WORKSPACE, "workspace too small");
+    MSST_REQUIRE(h.identity || workspace, MSST_ERR_INVALID_ARG, "null workspace");
+    MSST_REQUIRE(aligned(masks, 8) && aligned(stft, 8) && aligned(out, 8) &&
+                     (h.identity || aligned(workspace, 16)),
+                 MSST_ERR_ALIGNMENT, "8-byte alignment (workspace 16)");
+    if (batch == 0 || stems == 0 || frames == 0) return MSST_OK;
+    hipStream_t s = as_stream(stream);
+    const BandPlan* p = reinterpret_cast<const BandPlan*>(plan);
+    const float2* m = reinterpret_cast<const float2*>(masks);
+    if (!h.identity) {
+        float2* mg = reinterpret_cast<float2*>(workspace);
+        const int64_t rows = stems * batch * frames;
+        for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+            const int64_t nr = std::min<int64_t>(65535, rows - r0);
+            hipLaunchKernelGGL(mask_mean_kernel, dim3((unsigned)((h.nbins + 255) / 256), (unsigned)nr),
+                               dim3(256), 0, s, p, m + r0 * h.n_idx, mg + r0 * h.nbins);
+            rc = check_launch("mask_mean_kernel");
+            if (rc != MSST_OK) return rc;
+        }
+        m = mg;
+    }
+    const dim3 grid((unsigned)((frames + kTile - 1) / kTile), (unsigned)((h.nbins + kTile - 1) / kTile),
+                    (unsigned)(stems * batch));
+    hipLaunchKernelGGL(mask_apply_kernel, grid, dim3(256), 0, s, p, m,
+                       reinterpret_cast<const float2*>(stft), (int)batch, (int)frames, zero_dc,
+                       reinterpret_cast<float2*>(out));
+    return check_launch("mask_apply_kernel");
 }

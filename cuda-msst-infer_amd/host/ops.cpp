@@ -251,6 +251,9 @@ msst_band_config BandPlan::config() const {
     c.dim = dim_;
     c.hidden = hidden_;
     c.mlp_linears = linears_;
+    c.audio_channels = 0;  // the STFT side is not used through BandPlan
+    c.stft_bins = 0;
+    c.freq_indices = nullptr;
     return c;
 }
 

@@ -26,6 +26,13 @@
  *   msst_mask_estimator         model_bs_roformer.cu:374-414,
  *                               model_mel_band_roformer.cu:696-738 (per-band
  *                               linear/tanh MLP + glu + cat, ops.h:36, :116)
+ *   msst_band_gather            model_bs_roformer.cu:450-469,
+ *                               model_mel_band_roformer.cu:792-820 (stereo merge,
+ *                               index_select, permute into band features)
+ *   msst_mask_merge             model_bs_roformer.cu:551-590,
+ *                               model_mel_band_roformer.cu:924-1015 (stack,
+ *                               scatter_add + mean, complex_mul ops.h:51,
+ *                               stereo split, index_fill zero DC)
  *   msst_band_plan_init         the per-band weight tables of
  *                               model_bs_roformer.h:65-70, :105-115
  *   msst_rms_norm               ops.h:56               (ops_norm.cu:455-491)
@@ -257,6 +264,13 @@ typedef struct msst_band_config {
     int hidden;            /* mask-estimator hidden width (multiple of 64)    */
     int mlp_linears;       /* linears per band MLP (BSRoformer: mask_estimator_depth,
                               MelBandRoformer: mask_estimator_depth + 1); 1..8 */
+    /* STFT side (msst_band_gather / msst_mask_merge only; 0 / NULL otherwise): */
+    int audio_channels;    /* 1 or 2; bin g = f * audio_channels + s interleaves stereo */
+    int stft_bins;         /* F = n_fft / 2 + 1                                */
+    const int* freq_indices; /* host [sum(band_dims) / 2]: the interleaved bin of each band
+                              feature pair (MelBandRoformer's freq_indices_,
+                              model_mel_band_roformer.cu:238-268); NULL = bins in
+                              order, every bin once (BSRoformer)               */
 } msst_band_config;
 
 int64_t msst_band_plan_bytes(const msst_band_config* c);
@@ -291,6 +305,32 @@ int64_t msst_mask_estimator_workspace(const msst_band_config* c, int64_t rows);
 int msst_mask_estimator(const msst_band_config* c, const void* plan, const void* x,
                         int x_dtype, int64_t rows, float* out, void* workspace,
                         int64_t ws_bytes, void* stream);
+
+/* STFT -> band-split input (model_bs_roformer.cu:450-469,
+ * model_mel_band_roformer.cu:792-820: stereo merge into the bin axis, the
+ * freq_indices gather, complex folded into features):
+ *   out[b, t, 2 j + c] = stft[b * ch + s, f, t, c],  f * ch + s = freq_indices[j].
+ * stft f32 [batch * ch, F, frames, 2] (the STFT's layout), out f32
+ * [batch, frames, sum(band_dims)].  Needs the plan's STFT side. */
+int msst_band_gather(const msst_band_config* c, const void* plan, const float* stft,
+                     int64_t batch, int64_t frames, float* out, void* stream);
+
+/* Masks -> masked STFT, ready for the iSTFT (model_bs_roformer.cu:551-590,
+ * model_mel_band_roformer.cu:924-1015): each bin's mask is the mean over the
+ * bands that hold it (scatter_add / num_bands_per_freq, clamped at 1e-8; a
+ * plain copy for BSRoformer), complex-multiplied with the STFT, stereo
+ * un-interleaved, bin 0 zeroed when zero_dc:
+ *   out[(b * stems + n) * ch + s, f, t] = stft[b * ch + s, f, t] * mask_n[b, t, f * ch + s].
+ * masks f32 [stems][batch, frames, sum(band_dims)] (each stem's
+ * msst_mask_estimator output, stem-major), stft as above, out f32
+ * [batch * stems * ch, F, frames, 2].  The sums run in a fixed order
+ * (deterministic).  Workspace: msst_mask_merge_workspace bytes (0 for
+ * in-order bins), 16-byte aligned. */
+int64_t msst_mask_merge_workspace(const msst_band_config* c, int64_t batch, int64_t stems,
+                                  int64_t frames);
+int msst_mask_merge(const msst_band_config* c, const void* plan, const float* masks,
+                    int64_t stems, const float* stft, int64_t batch, int64_t frames,
+                    int zero_dc, float* out, void* workspace, int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

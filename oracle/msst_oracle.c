@@ -395,3 +395,56 @@ void orc_mask_estimator(const float* x, int64_t rows, const int* dims, int nb,
         off += d;
     }
 }
+
+/* model_bs_roformer.cu:450-469: permute [B,S,F,T,2] -> [B,F,S,T,2] (bins
+ * interleave channels), index_select on the bin axis, permute to [B,T,bins,2]. */
+void orc_band_gather(const float* stft, int64_t B, int64_t ch, int64_t F, int64_t T,
+                     const int* fidx, int64_t n, float* out) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t t = 0; t < T; ++t)
+            for (int64_t j = 0; j < n; ++j) {
+                const int64_t g = fidx ? fidx[j] : j;
+                const int64_t f = g / ch, s = g % ch;
+                const float* src = stft + (((b * ch + s) * F + f) * T + t) * 2;
+                out[((b * T + t) * n + j) * 2] = src[0];
+                out[((b * T + t) * n + j) * 2 + 1] = src[1];
+            }
+}
+
+/* model_mel_band_roformer.cu:924-1015: zeros, scatter_add (ops_misc.cu:395-440),
+ * masks_summed / clamp(num_bands_per_freq, 1e-8), complex_mul
+ * (ops_elementwise.cu:270-300), [B,N,F*S,T,2] -> [(B*N*S),F,T,2], index_fill. */
+void orc_mask_merge(const float* masks, int64_t stems, const float* stft, int64_t B,
+                    int64_t ch, int64_t F, int64_t T, const int* fidx, int64_t n,
+                    int zero_dc, float* out) {
+    const int64_t nbins = F * ch;
+    float* cnt = (float*)calloc((size_t)nbins, sizeof(float));
+    for (int64_t j = 0; j < n; ++j) cnt[fidx ? fidx[j] : j] += 1.0f;
+    float* sum = (float*)malloc((size_t)(nbins * T * 2) * sizeof(float));
+    for (int64_t nn = 0; nn < stems; ++nn)
+        for (int64_t b = 0; b < B; ++b) {
+            memset(sum, 0, (size_t)(nbins * T * 2) * sizeof(float));
+            const float* mk = masks + ((nn * B + b) * T) * n * 2;
+            for (int64_t t = 0; t < T; ++t)
+                for (int64_t j = 0; j < n; ++j) {
+                    const int64_t g = fidx ? fidx[j] : j;
+                    sum[(g * T + t) * 2] += mk[(t * n + j) * 2];
+                    sum[(g * T + t) * 2 + 1] += mk[(t * n + j) * 2 + 1];
+                }
+            for (int64_t g = 0; g < nbins; ++g) {
+                const int64_t f = g / ch, s = g % ch;
+                const float den = cnt[g] > 1e-8f ? cnt[g] : 1e-8f;
+                for (int64_t t = 0; t < T; ++t) {
+                    const float mr = sum[(g * T + t) * 2] / den, mi = sum[(g * T + t) * 2 + 1] / den;
+                    const float* x = stft + (((b * ch + s) * F + f) * T + t) * 2;
+                    float* o = out + ((((b * stems + nn) * ch + s) * F + f) * T + t) * 2;
+                    o[0] = x[0] * mr - x[1] * mi;
+                    o[1] = x[0] * mi + x[1] * mr;
+                    if (zero_dc && f == 0) o[0] = o[1] = 0.0f;
+                }
+            }
+        }
+    free(sum);
+    free(cnt);
+}

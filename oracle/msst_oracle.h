@@ -125,6 +125,24 @@ void orc_mask_estimator(const float* x, int64_t rows, const int* dims, int nb,
                         int64_t dim, int64_t hid, int L, const float* w,
                         const float* bias, float* out);
 
+/* STFT -> band features (model_bs_roformer.cu:450-469,
+ * model_mel_band_roformer.cu:792-820): stft [B*ch, F, T, 2]; the stereo
+ * channels are merged into the bin axis (g = f*ch + s), bins are gathered by
+ * fidx [n] (NULL: g = j) and complex is folded into the features:
+ * out[b, t, 2j + c] = stft[b*ch + s, f, t, c].  out [B, T, 2n]. */
+void orc_band_gather(const float* stft, int64_t B, int64_t ch, int64_t F, int64_t T,
+                     const int* fidx, int64_t n, float* out);
+
+/* Masks -> masked STFT (model_mel_band_roformer.cu:924-1015, and
+ * model_bs_roformer.cu:551-590 with fidx NULL): scatter_add of each stem's
+ * mask pairs into the bins, division by the number of bands per bin
+ * (clamped at 1e-8), complex_mul with the STFT, stereo un-interleave and
+ * index_fill of bin 0 when zero_dc.  masks [stems][B, T, 2n];
+ * out [(B*stems*ch), F, T, 2]. */
+void orc_mask_merge(const float* masks, int64_t stems, const float* stft, int64_t B,
+                    int64_t ch, int64_t F, int64_t T, const int* fidx, int64_t n,
+                    int zero_dc, float* out);
+
 #ifdef __cplusplus
 }
 #endif

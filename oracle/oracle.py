@@ -70,6 +70,9 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_band_split.argtypes = [_fp, _i64, _ip, ctypes.c_int, _fp, _fp, _fp, _fp, _i64]
     l.orc_mask_estimator.argtypes = [_fp, _i64, _ip, ctypes.c_int, _i64, _i64, ctypes.c_int,
                                      _fp, _fp, _fp]
+    l.orc_band_gather.argtypes = [_fp, _i64, _i64, _i64, _i64, _ip, _i64, _fp]
+    l.orc_mask_merge.argtypes = [_fp, _i64, _fp, _i64, _i64, _i64, _i64, _ip, _i64, ctypes.c_int,
+                                 _fp]
 
 
 def _f32(a) -> np.ndarray:
@@ -254,4 +257,37 @@ def mask_estimator(x, dims, ws, biases) -> np.ndarray:
     d, dp = _dims(dims)
     out = np.empty((rows, int(d.sum())), np.float32)
     lib().orc_mask_estimator(_p(x), rows, dp, nb, dim, hid, L, _p(w), _p(b), _p(out))
+    return out
+
+
+def _fidx(fidx):
+    if fidx is None:
+        return None, None
+    f = np.ascontiguousarray(fidx, dtype=np.int32)
+    return f, f.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+
+
+def band_gather(stft, batch, fidx=None) -> np.ndarray:
+    """stft [batch*ch, F, T, 2] -> [batch, T, 2n] (n = len(fidx) or F*ch)."""
+    stft = _f32(stft)
+    BC, F, T, _ = stft.shape
+    ch = BC // batch
+    f, fp = _fidx(fidx)
+    n = len(f) if f is not None else F * ch
+    out = np.empty((batch, T, 2 * n), np.float32)
+    lib().orc_band_gather(_p(stft), batch, ch, F, T, fp, n, _p(out))
+    return out
+
+
+def mask_merge(masks, stft, batch, fidx=None, zero_dc=True) -> np.ndarray:
+    """masks [stems, batch, T, 2n], stft [batch*ch, F, T, 2] -> [batch*stems*ch, F, T, 2]."""
+    masks, stft = _f32(masks), _f32(stft)
+    stems = masks.shape[0]
+    BC, F, T, _ = stft.shape
+    ch = BC // batch
+    f, fp = _fidx(fidx)
+    n = masks.shape[-1] // 2
+    out = np.empty((batch * stems * ch, F, T, 2), np.float32)
+    lib().orc_mask_merge(_p(masks), stems, _p(stft), batch, ch, F, T, fp, n, int(zero_dc),
+                         _p(out))
     return out

@@ -136,7 +136,7 @@ def test_product_does_not_reference_oracle():
 
 def _band_cfg(msst, dims, dim=64, hidden=128, L=2):
     arr = (ctypes.c_int * len(dims))(*dims)
-    return msst.BandConfig(len(dims), arr, dim, hidden, L), arr
+    return msst.BandConfig(len(dims), arr, dim, hidden, L, 0, 0, None), arr
 
 
 def test_band_config_validation(msst):

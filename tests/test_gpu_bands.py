@@ -137,3 +137,41 @@ def test_tanh_and_glu(msst, oracle, cuda, dt):
     g = host(msst.glu(dev(x, tdt)))
     assert g.shape == (333, 129)
     assert rel_err(g, oracle.glu(x)) < tol
+
+
+def _mel_like(F, ch, nb, seed):
+    """Overlapping contiguous bin ranges (as mel filters > 0 give), stereo
+    doubled (model_mel_band_roformer.cu:238-268)."""
+    rng = np.random.default_rng(seed)
+    edges = np.sort(rng.choice(np.arange(1, F - 1), nb - 1, replace=False))
+    lo = np.concatenate([[0], edges - 2])
+    hi = np.concatenate([edges + 2, [F - 1]])
+    fidx, dims = [], []
+    for a, b in zip(lo, hi):
+        bins = np.arange(max(a, 0), min(b, F - 1) + 1)
+        fidx.extend([int(f) * ch + s for f in bins for s in range(ch)])
+        dims.append(2 * len(bins) * ch)
+    return fidx, dims
+
+
+STFT_CASES = [("bsr", 1, 2, 1025, 801, 1, None), ("bsr-2stem", 2, 2, 1025, 130, 2, None),
+              ("mbr", 1, 2, 1025, 801, 1, 60), ("mbr-mono-3stem", 2, 1, 257, 70, 3, 20)]
+
+
+@pytest.mark.parametrize("name,B,ch,F,T,stems,mel", STFT_CASES, ids=[c[0] for c in STFT_CASES])
+def test_band_gather_and_mask_merge(msst, oracle, cuda, name, B, ch, F, T, stems, mel):
+    rng = np.random.default_rng(F + T)
+    if mel:
+        fidx, dims = _mel_like(F, ch, mel, 3)
+    else:
+        fidx, dims = None, [4 * f for f in BSR_FREQS] if (ch == 2 and F == 1025) else [2 * ch] * F
+    plan = msst.BandPlan(dims, 64, channels=ch, stft_bins=F, freq_indices=fidx)
+    stft = rng.standard_normal((B * ch, F, T, 2)).astype(np.float32)
+    feats = host(plan.band_gather(dev(stft), B))
+    np.testing.assert_array_equal(feats, oracle.band_gather(stft, B, fidx))
+    masks = rng.standard_normal((stems, B, T, sum(dims))).astype(np.float32)
+    for zero_dc in (True, False):
+        y = host(plan.mask_merge(dev(masks), dev(stft), B, zero_dc))
+        r = oracle.mask_merge(masks, stft, B, fidx, zero_dc)
+        assert y.shape == r.shape
+        assert rel_err(y, r) < 1e-6

@@ -323,3 +323,77 @@ def test_mask_estimator_gate_half_selects(oracle):
     for bi, d in enumerate(dims):
         v = oracle.linear(x[:, bi], ws[bi][0][:d], bs[bi][0][:d])
         np.testing.assert_allclose(y[:, off[bi]:off[bi + 1]], 0.5 * v, rtol=1e-6, atol=1e-7)
+
+
+# ------------------------------------------------------ STFT <-> band features
+def _mel_like_fidx(F, ch, nb, seed=0):
+    """Overlapping contiguous bin ranges per band (as mel filters > 0 give),
+    stereo-doubled the way model_mel_band_roformer.cu:255-268 builds them."""
+    rng = np.random.default_rng(seed)
+    edges = np.sort(rng.choice(np.arange(1, F - 1), nb - 1, replace=False))
+    lo = np.concatenate([[0], edges - 1])
+    hi = np.concatenate([edges + 1, [F - 1]])
+    fidx, dims = [], []
+    for a, b in zip(lo, hi):
+        bins = np.arange(max(a, 0), min(b, F - 1) + 1)
+        fidx.extend([int(f) * ch + s for f in bins for s in range(ch)])
+        dims.append(2 * len(bins) * ch)
+    return np.array(fidx, np.int32), dims
+
+
+@pytest.mark.parametrize("ch", [1, 2])
+def test_band_gather_is_stereo_interleave_then_index_select(oracle, ch):
+    B, F, T = 2, 9, 5
+    stft = rnd(B * ch, F, T, 2)
+    # 'b s f t c -> b t (f s) c' with numpy transposes
+    ref = stft.reshape(B, ch, F, T, 2).transpose(0, 3, 2, 1, 4).reshape(B, T, F * ch, 2)
+    np.testing.assert_array_equal(oracle.band_gather(stft, B), ref.reshape(B, T, -1))
+    fidx, _ = _mel_like_fidx(F, ch, 4)
+    np.testing.assert_array_equal(oracle.band_gather(stft, B, fidx),
+                                  ref[:, :, fidx].reshape(B, T, -1))
+
+
+@pytest.mark.parametrize("ch", [1, 2])
+@pytest.mark.parametrize("zero_dc", [False, True])
+def test_mask_merge_matches_scatter_mean_and_complex_product(oracle, ch, zero_dc):
+    B, F, T, stems = 2, 11, 6, 2
+    fidx, dims = _mel_like_fidx(F, ch, 5, seed=ch)
+    n = len(fidx)
+    stft = rnd(B * ch, F, T, 2)
+    masks = rnd(stems, B, T, 2 * n)
+    y = oracle.mask_merge(masks, stft, B, fidx, zero_dc)
+    # numpy: complex masks, np.add.at scatter, clamp-divide, complex multiply
+    mc = masks[..., 0::2] + 1j * masks[..., 1::2]                   # [stems, B, T, n]
+    acc = np.zeros((stems, B, T, F * ch), np.complex128)
+    np.add.at(acc, (slice(None), slice(None), slice(None), fidx), mc)
+    cnt = np.maximum(np.bincount(fidx, minlength=F * ch).astype(np.float64), 1e-8)
+    mean = acc / cnt                                                   # [stems, B, T, g]
+    xc = (stft[..., 0] + 1j * stft[..., 1]).reshape(B, ch, F, T)       # [B, s, f, t]
+    mg = mean.reshape(stems, B, T, F, ch).transpose(1, 0, 4, 3, 2)     # [B, stems, s, f, t]
+    o = xc[:, None] * mg
+    if zero_dc:
+        o[:, :, :, 0] = 0
+    ref = np.stack([o.real, o.imag], -1).reshape(B * stems * ch, F, T, 2)
+    assert rel_err(y, ref) < 1e-6
+
+
+def test_mask_merge_unit_mask_round_trips(oracle):
+    """Identity bins (BSRoformer) and a mask of 1 + 0i: the merge returns the
+    STFT itself (bin 0 zeroed), so gather and merge invert each other's
+    layout changes."""
+    B, ch, F, T = 1, 2, 7, 4
+    stft = rnd(B * ch, F, T, 2)
+    masks = np.zeros((1, B, T, 2 * F * ch), np.float32)
+    masks[..., 0::2] = 1.0
+    y = oracle.mask_merge(masks, stft, B, None, True)
+    ref = stft.copy()
+    ref[:, 0] = 0
+    np.testing.assert_array_equal(y, ref)
+    # the gathered features, conjugated, fed back as the mask: X * conj(X) =
+    # |X|^2 on every bin, imaginary part 0
+    feats = oracle.band_gather(stft, B)                     # [B, T, 2 * F * ch]
+    conj = feats.copy()
+    conj[..., 1::2] *= -1.0
+    y2 = oracle.mask_merge(conj[None], stft, B, None, False)
+    np.testing.assert_allclose(y2[..., 0], (stft ** 2).sum(-1), rtol=1e-6)
+    np.testing.assert_allclose(y2[..., 1], 0.0, atol=1e-6)
