@@ -269,8 +269,9 @@ BSR_FREQS = [2] * 24 + [4] * 12 + [12] * 8 + [24] * 8 + [48] * 8 + [128, 129]
 
 
 def band_table(msst, torch, B):
-    """Band split and one stem's mask estimator on one chunk's frames
-    (rows = B * 801), HIP-event timed, 50 launches after one warm-up."""
+    """Band gather, band split, one stem's mask estimator and the mask merge
+    on one chunk's frames (rows = B * 801), HIP-event timed, 50 launches
+    after one warm-up."""
     dims = [4 * f for f in BSR_FREQS]
     rows, nb, hid, ftot = B * FRAMES, len(dims), 4 * DIM, sum(dims)
     gen = torch.Generator(device="cuda").manual_seed(5)
@@ -282,10 +283,12 @@ def band_table(msst, torch, B):
              [n(DIM, dt=torch.float32) for d in dims])
     mask = ([[n(hid, DIM), n(2 * d, hid)] for d in dims],
             [[n(hid, dt=torch.float32), n(2 * d, dt=torch.float32)] for d in dims])
-    plan = msst.BandPlan(dims, DIM, split=split, mask=mask)
-    x = torch.randn(rows, ftot, device="cuda", generator=gen)
+    plan = msst.BandPlan(dims, DIM, split=split, mask=mask, channels=2, stft_bins=1025)
+    stft = torch.randn(2 * B, 1025, FRAMES, 2, device="cuda", generator=gen)
+    x = plan.band_gather(stft, B).reshape(rows, ftot)
     feats = plan.band_split(x)
     m = plan.mask_estimator(feats)
+    masks = m.reshape(1, B, FRAMES, ftot)
     out = {}
     f_split = 2.0 * rows * ftot * DIM
     f_mask = 2.0 * rows * nb * DIM * hid + 2.0 * rows * hid * 2 * ftot
@@ -293,15 +296,19 @@ def band_table(msst, torch, B):
             ("band_split", lambda: plan.band_split(x, out=feats), f_split,
              4 * rows * ftot + 4 * rows * nb * DIM + 2 * DIM * ftot),
             ("mask_estimator", lambda: plan.mask_estimator(feats, out=m), f_mask,
-             4 * rows * nb * DIM + 4 * rows * ftot + 2 * nb * hid * (DIM + 2 * 2 * ftot // nb))):
+             4 * rows * nb * DIM + 4 * rows * ftot + 2 * nb * hid * (DIM + 2 * 2 * ftot // nb)),
+            ("band_gather", lambda: plan.band_gather(stft, B), 0, 8 * rows * ftot),
+            ("mask_merge", lambda: plan.mask_merge(masks, stft, B), 0, 12 * rows * ftot)):
         fn()
         us = time_events(torch, fn, 50) / 50 * 1e3
-        tf = flops / (us * 1e-6) / 1e12
-        out[name] = {"us": round(us, 2), "tflops": round(tf, 1),
-                     "frac_mfma": round(tf / PEAK_F16_TFLOPS, 4),
-                     "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        e = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        if flops:
+            tf = flops / (us * 1e-6) / 1e12
+            e.update({"tflops": round(tf, 1), "frac_mfma": round(tf / PEAK_F16_TFLOPS, 4)})
+        out[name] = e
     out["config"] = f"BSRoformer bands: 62 bands, features {ftot}, rows {rows}, dim {DIM}, " \
-                    f"MLP {DIM}->{hid}->2*band, fp16 weights, fp32 input"
+                    f"MLP {DIM}->{hid}->2*band, fp16 weights, fp32 input; STFT side: " \
+                    f"stereo, 1025 bins, {FRAMES} frames, one stem"
     return out
 
 

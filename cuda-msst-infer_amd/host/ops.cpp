@@ -251,15 +251,16 @@ msst_band_config BandPlan::config() const {
     c.dim = dim_;
     c.hidden = hidden_;
     c.mlp_linears = linears_;
-    c.audio_channels = 0;  // the STFT side is not used through BandPlan
-    c.stft_bins = 0;
-    c.freq_indices = nullptr;
+    c.audio_channels = stft_.channels;
+    c.stft_bins = stft_.stft_bins;
+    c.freq_indices = stft_.freq_indices.empty() ? nullptr : stft_.freq_indices.data();
     return c;
 }
 
 BandPlan::BandPlan(std::vector<int> band_dims, int dim, const BandSplitWeights* split,
-                   const MaskEstimatorWeights* mask)
+                   const MaskEstimatorWeights* mask, const StftBands* stft)
     : dims_(std::move(band_dims)), dim_(dim) {
+    if (stft) stft_ = *stft;
     const size_t nb = dims_.size();
     if (mask) {
         if (mask->w.size() != nb || mask->b.size() != nb || mask->w[0].empty())
@@ -320,6 +321,46 @@ BandPlan::BandPlan(std::vector<int> band_dims, int dim, const BandSplitWeights* 
                               split ? sb.data() : nullptr, mask ? mw.data() : nullptr,
                               mask ? mb.data() : nullptr, plan_.data_ptr(), bytes, stream()),
           "BandPlan");
+}
+
+Tensor BandPlan::band_gather(const Tensor& stft, int64_t batch) const {
+    if (stft_.channels == 0) throw std::runtime_error("band_gather: plan has no STFT side");
+    if (stft.ndim() != 4 || stft.dtype() != DType::Float32 || stft.size(3) != 2 ||
+        stft.size(0) != batch * stft_.channels || stft.size(1) != stft_.stft_bins)
+        throw std::runtime_error("band_gather: stft must be fp32 [batch * channels, F, T, 2]");
+    int64_t ftot = 0;
+    for (int d : dims_) ftot += d;
+    const int64_t T = stft.size(2);
+    Tensor out = Tensor::empty({batch, T, ftot}, DType::Float32);
+    const msst_band_config c = config();
+    check(msst_band_gather(&c, plan_.data_ptr(), stft.data_f32(), batch, T, out.data_f32(),
+                           stream()),
+          "band_gather");
+    return out;
+}
+
+Tensor BandPlan::mask_merge(const Tensor& masks, const Tensor& stft, int64_t batch,
+                            bool zero_dc) const {
+    if (stft_.channels == 0) throw std::runtime_error("mask_merge: plan has no STFT side");
+    int64_t ftot = 0;
+    for (int d : dims_) ftot += d;
+    if (stft.ndim() != 4 || stft.dtype() != DType::Float32 || stft.size(3) != 2 ||
+        stft.size(0) != batch * stft_.channels || stft.size(1) != stft_.stft_bins)
+        throw std::runtime_error("mask_merge: stft must be fp32 [batch * channels, F, T, 2]");
+    const int64_t T = stft.size(2);
+    if (masks.ndim() != 4 || masks.dtype() != DType::Float32 || masks.size(1) != batch ||
+        masks.size(2) != T || masks.size(3) != ftot)
+        throw std::runtime_error("mask_merge: masks must be fp32 [stems, batch, T, sum(dims)]");
+    const int64_t stems = masks.size(0);
+    Tensor out = Tensor::empty({batch * stems * stft_.channels, (int64_t)stft_.stft_bins, T, 2},
+                               DType::Float32);
+    const msst_band_config c = config();
+    const int64_t wsb = msst_mask_merge_workspace(&c, batch, stems, T);
+    Tensor ws = Tensor::empty({std::max<int64_t>((wsb + 3) / 4, 1)}, DType::Float32);
+    check(msst_mask_merge(&c, plan_.data_ptr(), masks.data_f32(), stems, stft.data_f32(), batch,
+                          T, zero_dc ? 1 : 0, out.data_f32(), ws.data_ptr(), wsb, stream()),
+          "mask_merge");
+    return out;
 }
 
 Tensor BandPlan::band_split(const Tensor& x) const {

@@ -114,11 +114,29 @@ struct MaskEstimatorWeights {
     std::vector<std::vector<Tensor>> w, b;  // [band][layer]
 };
 
+// The STFT side of the bands: channels (1/2), STFT bins F, and the
+// interleaved bin (f * channels + s) of every band feature pair
+// (MelBandRoformer's freq_indices_, model_mel_band_roformer.cu:238-268);
+// empty freq_indices = every bin once, in order (BSRoformer).
+struct StftBands {
+    int channels = 0;
+    int stft_bins = 0;
+    std::vector<int> freq_indices;
+};
+
 class BandPlan {
 public:
     // Either weight set may be null.  The tensors must outlive the plan.
     BandPlan(std::vector<int> band_dims, int dim, const BandSplitWeights* split,
-             const MaskEstimatorWeights* mask);
+             const MaskEstimatorWeights* mask, const StftBands* stft = nullptr);
+    // STFT [B * ch, F, T, 2] -> band-split input [B, T, sum(band_dims)]
+    // (stereo merge, index_select, permute; model_bs_roformer.cu:450-469).
+    Tensor band_gather(const Tensor& stft, int64_t batch) const;
+    // Stem masks [stems, B, T, sum(band_dims)] and the STFT -> masked STFT
+    // [B * stems * ch, F, T, 2] for the iSTFT (scatter_add mean, complex_mul,
+    // stereo split, zero DC; model_mel_band_roformer.cu:924-1015).
+    Tensor mask_merge(const Tensor& masks, const Tensor& stft, int64_t batch,
+                      bool zero_dc) const;
     // x [..., sum(band_dims)] fp32 -> [..., num_bands, dim] fp32
     // (apply_band_split: split, rms_norm * sqrt(fd), linear, stack).
     Tensor band_split(const Tensor& x) const;
@@ -129,6 +147,7 @@ public:
 private:
     std::vector<int> dims_;
     int dim_ = 0, hidden_ = 0, linears_ = 1;
+    StftBands stft_;
     Tensor plan_;
     std::vector<Tensor> keep_;  // fp32 copies of fp16 gammas / biases
     msst_band_config config() const;

@@ -326,6 +326,35 @@ static void test_bands() {
     });
     expect_throw("mask_estimator on the wrong band count",
                  [&] { plan.mask_estimator(Tensor::zeros({rows, nb + 1, dim})); });
+
+    // STFT side: overlapping bands over 9 stereo bins, gather then merge.
+    {
+        const int F = 9, ch = 2, Tn = 5, Bb = 2, stems = 2;
+        ops::StftBands sb;
+        sb.channels = ch;
+        sb.stft_bins = F;
+        std::vector<int> bd;
+        for (int lo : {0, 3, 5}) {  // bands over bins [0,4), [3,6), [5,9)
+            const int hi = lo == 0 ? 4 : lo == 3 ? 6 : 9;
+            for (int f = lo; f < hi; ++f)
+                for (int s2 = 0; s2 < ch; ++s2) sb.freq_indices.push_back(f * ch + s2);
+            bd.push_back(2 * (hi - lo) * ch);
+        }
+        ops::BandPlan sp(bd, 64, nullptr, nullptr, &sb);
+        const int n = (int)sb.freq_indices.size();
+        auto st = randn((size_t)Bb * ch * F * Tn * 2, 1.0f, 91);
+        Tensor std_ = dev(st, {Bb * ch, F, Tn, 2}, DType::Float32);
+        std::vector<float> rg((size_t)Bb * Tn * 2 * n);
+        orc_band_gather(st.data(), Bb, ch, F, Tn, sb.freq_indices.data(), n, rg.data());
+        check_close("band_gather", sp.band_gather(std_, Bb), rg, 0.0);
+        auto mk = randn((size_t)stems * Bb * Tn * 2 * n, 1.0f, 92);
+        std::vector<float> rm((size_t)Bb * stems * ch * F * Tn * 2);
+        orc_mask_merge(mk.data(), stems, st.data(), Bb, ch, F, Tn, sb.freq_indices.data(), n, 1,
+                       rm.data());
+        check_close("mask_merge", sp.mask_merge(dev(mk, {stems, Bb, Tn, 2 * n}, DType::Float32),
+                                               std_, Bb, true),
+                    rm, 1e-6);
+    }
 }
 
 int main() {

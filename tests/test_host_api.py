@@ -29,6 +29,8 @@ SIGNATURES = [
     "cudasep::ops::glu(cudasep::Tensor const&, int)",
     "cudasep::ops::BandPlan::band_split(cudasep::Tensor const&) const",
     "cudasep::ops::BandPlan::mask_estimator(cudasep::Tensor const&) const",
+    "cudasep::ops::BandPlan::band_gather(cudasep::Tensor const&, long) const",
+    "cudasep::ops::BandPlan::mask_merge(cudasep::Tensor const&, cudasep::Tensor const&, long, bool) const",
     "cudasep::clear_attention_graph_cache()",
     "cudasep::CudaContext::instance()",
     "cudasep::Tensor::empty(std::vector<long, std::allocator<long> >, cudasep::DType)",
