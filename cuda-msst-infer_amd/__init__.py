@@ -103,6 +103,12 @@ _SIGS = {
     "msst_band_gather": ([_BCP, _vp, _vp, _i64, _i64, _vp, _vp], _int),
     "msst_mask_merge_workspace": ([_BCP, _i64, _i64, _i64], _i64),
     "msst_mask_merge": ([_BCP, _vp, _vp, _i64, _vp, _i64, _i64, _int, _vp, _vp, _i64, _vp], _int),
+    "msst_stft_frames": ([_i64, _int, _int, _int], _i64),
+    "msst_stft": ([_vp, _i64, _i64, _int, _int, _vp, _int, _int, _vp, _vp], _int),
+    "msst_istft_length": ([_i64, _int, _int, _i64, _int], _i64),
+    "msst_istft_workspace": ([_i64, _i64, _int], _i64),
+    "msst_istft": ([_vp, _i64, _i64, _int, _int, _vp, _i64, _int, _int, _vp, _vp, _i64, _vp], _int),
+    "msst_hann_window": ([_vp, _int, _vp], _int),
     "msst_roformer_transformer": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights),
                                    _int, _vp, _i64, _vp], _int),
 }
@@ -349,6 +355,42 @@ class RoformerStack:
             _ptr(self.workspace), self.workspace.numel(), _stream()),
             "msst_roformer_transformer")
         return x
+
+
+def hann_window(size: int, device="cuda"):
+    import torch
+    out = torch.empty(size, device=device)
+    check(lib().msst_hann_window(_ptr(out), size, _stream()), "msst_hann_window")
+    return out
+
+
+def stft(signal, n_fft, hop, window, center=True, normalized=False):
+    """signal f32 [B, L] -> [B, n_fft/2 + 1, T, 2] (torch.stft semantics)."""
+    import torch
+    B, L = signal.shape
+    T = lib().msst_stft_frames(L, n_fft, hop, int(center))
+    if T < 1:
+        raise MsstError("msst_stft_frames: n_fft must be a power of two in [16, 4096], hop >= 1, "
+                        "and the signal long enough for one frame (centre: L > n_fft / 2)")
+    out = torch.empty(B, n_fft // 2 + 1, T, 2, device=signal.device)
+    check(lib().msst_stft(_ptr(signal), B, L, n_fft, hop, _ptr(window), int(center),
+                          int(normalized), _ptr(out), _stream()), "msst_stft")
+    return out
+
+
+def istft(spec, n_fft, hop, window, length=-1, center=True, normalized=False):
+    """spec f32 [B, n_fft/2 + 1, T, 2] -> [B, out_len] (torch.istft semantics)."""
+    import torch
+    B, F, T, _ = spec.shape
+    n = lib().msst_istft_length(T, n_fft, hop, length, int(center))
+    if n < 1:
+        raise MsstError("msst_istft_length: bad n_fft / hop / frames / length")
+    out = torch.empty(B, n, device=spec.device)
+    wsb = lib().msst_istft_workspace(B, T, n_fft)
+    ws = torch.empty(max(int(wsb), 16), dtype=torch.uint8, device=spec.device)
+    check(lib().msst_istft(_ptr(spec), B, T, n_fft, hop, _ptr(window), length, int(center),
+                           int(normalized), _ptr(out), _ptr(ws), wsb, _stream()), "msst_istft")
+    return out
 
 
 def tanh(x, out=None):

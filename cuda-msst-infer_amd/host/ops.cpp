@@ -101,6 +101,54 @@ Tensor rms_norm(const Tensor& x, const Tensor& gamma, float scale) {
     return out;
 }
 
+// ops_stft.cu:286-362
+Tensor stft(const Tensor& signal, int n_fft, int hop_length, int win_length,
+            const Tensor& window, bool center, bool normalized) {
+    if (win_length != n_fft || window.numel() != n_fft)
+        throw std::runtime_error("stft: the window must have n_fft samples");
+    Tensor sig = f32(signal);
+    if (sig.ndim() == 1) sig = sig.reshape({1, sig.size(0)});
+    if (sig.ndim() != 2) throw std::runtime_error("stft: signal must be [B, L] or [L]");
+    const int64_t B = sig.size(0), L = sig.size(1);
+    const int64_t T = msst_stft_frames(L, n_fft, hop_length, center ? 1 : 0);
+    if (T < 1) throw std::runtime_error("stft: signal too short or bad n_fft / hop");
+    Tensor w = f32(window);
+    Tensor out = Tensor::empty({B, (int64_t)n_fft / 2 + 1, T, 2}, DType::Float32);
+    check(msst_stft(sig.data_f32(), B, L, n_fft, hop_length, w.data_f32(), center ? 1 : 0,
+                    normalized ? 1 : 0, out.data_f32(), stream()),
+          "stft");
+    return out;
+}
+
+// ops_stft.cu:368-491
+Tensor istft(const Tensor& complex_spec, int n_fft, int hop_length, int win_length,
+             const Tensor& window, int64_t length, bool center, bool normalized) {
+    if (win_length != n_fft || window.numel() != n_fft)
+        throw std::runtime_error("istft: the window must have n_fft samples");
+    Tensor spec = f32(complex_spec);
+    if (spec.ndim() != 4 || spec.size(1) != n_fft / 2 + 1 || spec.size(3) != 2)
+        throw std::runtime_error("istft: spec must be [B, n_fft/2 + 1, T, 2]");
+    const int64_t B = spec.size(0), T = spec.size(2);
+    const int64_t n = msst_istft_length(T, n_fft, hop_length, length, center ? 1 : 0);
+    if (n < 1) throw std::runtime_error("istft: bad n_fft / hop / length");
+    Tensor w = f32(window);
+    Tensor out = Tensor::empty({B, n}, DType::Float32);
+    const int64_t wsb = msst_istft_workspace(B, T, n_fft);
+    Tensor ws = Tensor::empty({std::max<int64_t>((wsb + 3) / 4, 1)}, DType::Float32);
+    check(msst_istft(spec.data_f32(), B, T, n_fft, hop_length, w.data_f32(), length,
+                     center ? 1 : 0, normalized ? 1 : 0, out.data_f32(), ws.data_ptr(), wsb,
+                     stream()),
+          "istft");
+    return out;
+}
+
+// ops_stft.cu:264-280
+Tensor hann_window(int size) {
+    Tensor out = Tensor::empty({(int64_t)std::max(size, 0)}, DType::Float32);
+    if (size > 0) check(msst_hann_window(out.data_f32(), size, stream()), "hann_window");
+    return out;
+}
+
 // ops_elementwise.cu:84-88, :138
 Tensor tanh_act(const Tensor& x) {
     Tensor out = Tensor::empty(x.shape(), x.dtype());

@@ -70,6 +70,18 @@ Tensor scaled_dot_product_attention(const Tensor& q, const Tensor& k, const Tens
 // q,k: [B, H, N, D] rotated in place (interleaved pairs); cos/sin [N, D/2].
 void apply_rotary_emb(Tensor& q, Tensor& k, const Tensor& cos_freqs, const Tensor& sin_freqs);
 
+// ops.h:87-96 (ops_stft.cu): torch.stft / torch.istft semantics on a
+// hand-written FFT (power-of-two n_fft in [16, 4096]; win_length must equal
+// n_fft, as the reference's kernels index the window by n_fft).
+// stft: signal [B, L] (or [L]) -> [B, n_fft/2 + 1, T, 2] fp32.
+// istft: [B, F, T, 2] -> [B, length or the full trimmed length] fp32.
+Tensor stft(const Tensor& signal, int n_fft, int hop_length, int win_length,
+            const Tensor& window, bool center = true, bool normalized = false);
+Tensor istft(const Tensor& complex_spec, int n_fft, int hop_length, int win_length,
+             const Tensor& window, int64_t length = -1, bool center = true,
+             bool normalized = false);
+Tensor hann_window(int size);
+
 // ops_elementwise.cu:84-88, :138 (tanhf) and :321-388 (first * sigmoid(second));
 // glu splits the last dimension only (the Roformers' use, dim = -1).
 Tensor tanh_act(const Tensor& x);

@@ -33,6 +33,9 @@
  *                               model_mel_band_roformer.cu:924-1015 (stack,
  *                               scatter_add + mean, complex_mul ops.h:51,
  *                               stereo split, index_fill zero DC)
+ *   msst_stft                   ops.h:87-89   (ops_stft.cu:286-362, cuFFT R2C)
+ *   msst_istft                  ops.h:91-93   (ops_stft.cu:368-491, cuFFT C2R)
+ *   msst_hann_window            ops.h:96      (ops_stft.cu:268-280)
  *   msst_band_plan_init         the per-band weight tables of
  *                               model_bs_roformer.h:65-70, :105-115
  *   msst_rms_norm               ops.h:56               (ops_norm.cu:455-491)
@@ -331,6 +334,34 @@ int64_t msst_mask_merge_workspace(const msst_band_config* c, int64_t batch, int6
 int msst_mask_merge(const msst_band_config* c, const void* plan, const float* masks,
                     int64_t stems, const float* stft, int64_t batch, int64_t frames,
                     int zero_dc, float* out, void* workspace, int64_t ws_bytes, void* stream);
+
+/* ---- STFT / iSTFT (torch.stft / torch.istft semantics, as the reference) --
+ * Hand-written FFT (power-of-two n_fft in [16, 4096]); the window has n_fft
+ * samples (win_length == n_fft, as the reference's kernels index it).
+ *
+ * out[b, k, t] = sum_n x_b[t * hop + n - pad] w[n] exp(-2 pi i k n / n_fft),
+ * k = 0..n_fft/2, pad = n_fft/2 with reflect padding when center (needs
+ * length > n_fft/2), times 1/sqrt(n_fft) when normalized.  signal f32
+ * [batch, length], out f32 [batch, n_fft/2 + 1, frames, 2] with frames =
+ * msst_stft_frames(...). */
+int64_t msst_stft_frames(int64_t length, int n_fft, int hop, int center);
+int msst_stft(const float* signal, int64_t batch, int64_t length, int n_fft, int hop,
+              const float* window, int center, int normalized, float* out, void* stream);
+
+/* Inverse: per frame the Hermitian C2R transform (imaginary parts of bins 0
+ * and n_fft/2 ignored) / n_fft, windowed, overlap-added in frame order and
+ * divided by sum_t w^2 where that exceeds 1e-8; the centre padding is
+ * trimmed and the result truncated or zero-padded to `length` (> 0), else
+ * msst_istft_length(...) samples.  spec f32 [batch, n_fft/2 + 1, frames, 2],
+ * out f32 [batch, out_len].  Workspace: msst_istft_workspace bytes. */
+int64_t msst_istft_length(int64_t frames, int n_fft, int hop, int64_t length, int center);
+int64_t msst_istft_workspace(int64_t batch, int64_t frames, int n_fft);
+int msst_istft(const float* spec, int64_t batch, int64_t frames, int n_fft, int hop,
+               const float* window, int64_t length, int center, int normalized, float* out,
+               void* workspace, int64_t ws_bytes, void* stream);
+
+/* Periodic Hann window, w[i] = (1 - cos(2 pi i / size)) / 2 (size 1: 1). */
+int msst_hann_window(float* out, int size, void* stream);
 
 #ifdef __cplusplus
 }

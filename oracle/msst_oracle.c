@@ -448,3 +448,114 @@ void orc_mask_merge(const float* masks, int64_t stems, const float* stft, int64_
     free(sum);
     free(cnt);
 }
+
+/* In-place iterative radix-2 complex FFT in float64 (n a power of two);
+ * sign -1 forward, +1 inverse (unnormalised). */
+static void fft64(double* re, double* im, int n, int sign) {
+    for (int i = 1, j = 0; i < n; ++i) {
+        int bit = n >> 1;
+        for (; j & bit; bit >>= 1) j ^= bit;
+        j ^= bit;
+        if (i < j) {
+            double t = re[i]; re[i] = re[j]; re[j] = t;
+            t = im[i]; im[i] = im[j]; im[j] = t;
+        }
+    }
+    for (int len = 2; len <= n; len <<= 1) {
+        const double ang = sign * 2.0 * 3.14159265358979323846 / len;
+        for (int i = 0; i < n; i += len)
+            for (int k = 0; k < len / 2; ++k) {
+                const double wr = cos(ang * k), wi = sin(ang * k);
+                const int a = i + k, b = i + k + len / 2;
+                const double xr = re[b] * wr - im[b] * wi, xi = re[b] * wi + im[b] * wr;
+                re[b] = re[a] - xr; im[b] = im[a] - xi;
+                re[a] += xr; im[a] += xi;
+            }
+    }
+}
+
+/* ops_stft.cu:286-362: pad_reflect, extract_frames_kernel, apply_window_kernel,
+ * cufftExecR2C, complex_to_real_imag_kernel, stft_scale_kernel. */
+void orc_stft(const float* signal, int64_t B, int64_t L, int n_fft, int hop,
+              const float* window, int center, int normalized, float* out) {
+    const int64_t pad = center ? n_fft / 2 : 0;
+    const int64_t T = (L + 2 * pad - n_fft) / hop + 1;
+    const int F = n_fft / 2 + 1;
+    const double scale = normalized ? 1.0 / sqrt((double)n_fft) : 1.0;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t t = 0; t < T; ++t) {
+            double* re = (double*)malloc(sizeof(double) * n_fft);
+            double* im = (double*)malloc(sizeof(double) * n_fft);
+            for (int n = 0; n < n_fft; ++n) {
+                int64_t p = t * hop + n - pad;
+                if (p < 0) p = -p;
+                if (p >= L) p = 2 * (L - 1) - p;
+                re[n] = (double)signal[b * L + p] * (double)window[n];
+                im[n] = 0.0;
+            }
+            fft64(re, im, n_fft, -1);
+            for (int k = 0; k < F; ++k) {
+                float* o = out + ((b * F + k) * T + t) * 2;
+                o[0] = (float)(re[k] * scale);
+                o[1] = (float)(im[k] * scale);
+            }
+            free(re);
+            free(im);
+        }
+}
+
+/* ops_stft.cu:368-491: real_imag_to_complex, cufftExecC2R, / n_fft,
+ * apply_window_kernel, overlap_add_kernel, window_sum_kernel,
+ * normalize_by_window_kernel, centre slice, pad / slice to length. */
+void orc_istft(const float* spec, int64_t B, int64_t T, int n_fft, int hop,
+               const float* window, int64_t out_len, int center, int normalized, float* out) {
+    const int F = n_fft / 2 + 1;
+    const int64_t full = (int64_t)n_fft + (T - 1) * hop;
+    const int64_t pad = center ? n_fft / 2 : 0;
+    const double scale = normalized ? sqrt((double)n_fft) : 1.0;
+    double* ola = (double*)calloc((size_t)(B * full), sizeof(double));
+    double* wsum = (double*)calloc((size_t)full, sizeof(double));
+    for (int64_t t = 0; t < T; ++t)
+        for (int n = 0; n < n_fft; ++n) wsum[t * hop + n] += (double)window[n] * window[n];
+#pragma omp parallel for schedule(static)
+    for (int64_t b = 0; b < B; ++b) {
+        double* re = (double*)malloc(sizeof(double) * n_fft);
+        double* im = (double*)malloc(sizeof(double) * n_fft);
+        for (int64_t t = 0; t < T; ++t) {
+            for (int k = 0; k < F; ++k) {
+                const float* s = spec + ((b * F + k) * T + t) * 2;
+                re[k] = s[0] * scale;
+                im[k] = (k == 0 || k == F - 1) ? 0.0 : s[1] * scale;
+            }
+            for (int k = F; k < n_fft; ++k) {  /* Hermitian extension */
+                re[k] = re[n_fft - k];
+                im[k] = -im[n_fft - k];
+            }
+            fft64(re, im, n_fft, +1);
+            for (int n = 0; n < n_fft; ++n)
+                ola[b * full + t * hop + n] += re[n] / n_fft * window[n];
+        }
+        free(re);
+        free(im);
+    }
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t o = 0; o < out_len; ++o) {
+            const int64_t pos = o + pad;
+            double v = 0.0;
+            if (pos < full - pad) {
+                v = ola[b * full + pos];
+                if (wsum[pos] > 1e-8) v /= wsum[pos];
+            }
+            out[b * out_len + o] = (float)v;
+        }
+    free(ola);
+    free(wsum);
+}
+
+/* ops_stft.cu:254-262 (periodic Hann, hann_window size 1 -> 1). */
+void orc_hann_window(float* out, int size) {
+    for (int i = 0; i < size; ++i)
+        out[i] = size == 1 ? 1.0f
+                           : (float)(0.5 * (1.0 - cos(2.0 * 3.14159265358979323846 * i / size)));
+}

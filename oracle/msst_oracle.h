@@ -143,6 +143,23 @@ void orc_mask_merge(const float* masks, int64_t stems, const float* stft, int64_
                     int64_t ch, int64_t F, int64_t T, const int* fidx, int64_t n,
                     int zero_dc, float* out);
 
+/* torch.stft semantics (ops_stft.cu:286-362): reflect-pad n_fft/2 each side
+ * when center, frames at hop, window [n_fft], one-sided FFT (float64 radix-2
+ * here), times 1/sqrt(n_fft) when normalized.  signal [B, L] ->
+ * out [B, n_fft/2 + 1, T, 2], T = (L + (center ? n_fft : 0) - n_fft) / hop + 1. */
+void orc_stft(const float* signal, int64_t B, int64_t L, int n_fft, int hop,
+              const float* window, int center, int normalized, float* out);
+
+/* torch.istft semantics (ops_stft.cu:368-491): C2R per frame / n_fft (imaginary
+ * parts of bins 0 and n_fft/2 ignored), window, overlap-add, division by the
+ * squared-window sum where > 1e-8, centre trim, truncate / zero-pad to
+ * `length` (> 0).  spec [B, n_fft/2 + 1, T, 2] -> out [B, out_len]. */
+void orc_istft(const float* spec, int64_t B, int64_t T, int n_fft, int hop,
+               const float* window, int64_t out_len, int center, int normalized, float* out);
+
+/* Periodic Hann window (ops_stft.cu:254-262). */
+void orc_hann_window(float* out, int size);
+
 #ifdef __cplusplus
 }
 #endif

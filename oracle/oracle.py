@@ -71,6 +71,11 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_mask_estimator.argtypes = [_fp, _i64, _ip, ctypes.c_int, _i64, _i64, ctypes.c_int,
                                      _fp, _fp, _fp]
     l.orc_band_gather.argtypes = [_fp, _i64, _i64, _i64, _i64, _ip, _i64, _fp]
+    l.orc_stft.argtypes = [_fp, _i64, _i64, ctypes.c_int, ctypes.c_int, _fp, ctypes.c_int,
+                           ctypes.c_int, _fp]
+    l.orc_istft.argtypes = [_fp, _i64, _i64, ctypes.c_int, ctypes.c_int, _fp, _i64, ctypes.c_int,
+                            ctypes.c_int, _fp]
+    l.orc_hann_window.argtypes = [_fp, ctypes.c_int]
     l.orc_mask_merge.argtypes = [_fp, _i64, _fp, _i64, _i64, _i64, _i64, _ip, _i64, ctypes.c_int,
                                  _fp]
 
@@ -290,4 +295,33 @@ def mask_merge(masks, stft, batch, fidx=None, zero_dc=True) -> np.ndarray:
     out = np.empty((batch * stems * ch, F, T, 2), np.float32)
     lib().orc_mask_merge(_p(masks), stems, _p(stft), batch, ch, F, T, fp, n, int(zero_dc),
                          _p(out))
+    return out
+
+
+def hann_window(size: int) -> np.ndarray:
+    out = np.empty(size, np.float32)
+    lib().orc_hann_window(_p(out), size)
+    return out
+
+
+def stft(signal, n_fft, hop, window, center=True, normalized=False) -> np.ndarray:
+    """signal [B, L] -> [B, n_fft/2 + 1, T, 2]."""
+    x = _f32(signal)
+    B, L = x.shape
+    w = _f32(window)
+    T = (L + (n_fft if center else 0) - n_fft) // hop + 1
+    out = np.empty((B, n_fft // 2 + 1, T, 2), np.float32)
+    lib().orc_stft(_p(x), B, L, n_fft, hop, _p(w), int(center), int(normalized), _p(out))
+    return out
+
+
+def istft(spec, n_fft, hop, window, length=-1, center=True, normalized=False) -> np.ndarray:
+    """spec [B, n_fft/2 + 1, T, 2] -> [B, out_len]."""
+    s = _f32(spec)
+    B, F, T, _ = s.shape
+    w = _f32(window)
+    out_len = length if length > 0 else n_fft + (T - 1) * hop - (n_fft if center else 0)
+    out = np.empty((B, out_len), np.float32)
+    lib().orc_istft(_p(s), B, T, n_fft, hop, _p(w), out_len, int(center), int(normalized),
+                    _p(out))
     return out

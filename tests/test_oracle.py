@@ -397,3 +397,114 @@ def test_mask_merge_unit_mask_round_trips(oracle):
     y2 = oracle.mask_merge(conj[None], stft, B, None, False)
     np.testing.assert_allclose(y2[..., 0], (stft ** 2).sum(-1), rtol=1e-6)
     np.testing.assert_allclose(y2[..., 1], 0.0, atol=1e-6)
+
+
+# ----------------------------------------------------------------- STFT / iSTFT
+def _np_stft(x, n_fft, hop, w, center, normalized):
+    """torch.stft restated with numpy: reflect pad, frames, window, rfft."""
+    if center:
+        x = np.pad(x, ((0, 0), (n_fft // 2, n_fft // 2)), mode="reflect")
+    T = (x.shape[1] - n_fft) // hop + 1
+    idx = np.arange(T)[:, None] * hop + np.arange(n_fft)[None]
+    X = np.fft.rfft(x[:, idx].astype(np.float64) * w, axis=-1)        # [B, T, F]
+    if normalized:
+        X = X / np.sqrt(n_fft)
+    return np.stack([X.real, X.imag], -1).transpose(0, 2, 1, 3)      # [B, F, T, 2]
+
+
+def test_hann_window_is_periodic_hann(oracle):
+    for n in (1, 2, 16, 2048):
+        ref = np.hanning(n + 1)[:-1] if n > 1 else np.ones(1)
+        np.testing.assert_allclose(oracle.hann_window(n), ref, atol=1e-7)
+
+
+@pytest.mark.parametrize("n_fft,hop,L", [(16, 4, 50), (64, 17, 300), (256, 64, 1000),
+                                         (2048, 441, 5000)])
+@pytest.mark.parametrize("center", [True, False])
+@pytest.mark.parametrize("normalized", [False, True])
+def test_stft_matches_numpy_rfft(oracle, n_fft, hop, L, center, normalized):
+    x = rnd(2, L)
+    w = oracle.hann_window(n_fft)
+    y = oracle.stft(x, n_fft, hop, w, center, normalized)
+    r = _np_stft(x, n_fft, hop, w.astype(np.float64), center, normalized)
+    assert y.shape == r.shape
+    assert rel_err(y, r) < 1e-6
+
+
+def test_stft_closed_forms(oracle):
+    """A unit impulse at frame centre with a rectangular window has a flat
+    spectrum whose phase turns by -2 pi k n0 / N; a cosine at bin k0 lands
+    on bins k0 only (N/2 each side of the real part)."""
+    n_fft = 64
+    x = np.zeros((1, 200), np.float32)
+    x[0, 100] = 1.0
+    w = np.ones(n_fft, np.float32)
+    y = oracle.stft(x, n_fft, 100, w, center=True)            # frame 1 covers samples 68..131
+    n0 = 100 - (100 - n_fft // 2)
+    k = np.arange(n_fft // 2 + 1)
+    np.testing.assert_allclose(y[0, :, 1, 0], np.cos(-2 * np.pi * k * n0 / n_fft), atol=1e-6)
+    np.testing.assert_allclose(y[0, :, 1, 1], np.sin(-2 * np.pi * k * n0 / n_fft), atol=1e-6)
+    k0 = 5
+    c = np.cos(2 * np.pi * k0 * np.arange(n_fft) / n_fft).astype(np.float32)[None]
+    z = oracle.stft(c, n_fft, n_fft, w, center=False)[0, :, 0]
+    expect = np.zeros_like(z)
+    expect[k0, 0] = n_fft / 2
+    np.testing.assert_allclose(z, expect, atol=1e-5)
+
+
+@pytest.mark.parametrize("n_fft,hop,L", [(64, 16, 400), (256, 100, 3000), (2048, 441, 20000)])
+@pytest.mark.parametrize("center", [True, False])
+def test_istft_inverts_stft(oracle, n_fft, hop, L, center):
+    """Perfect reconstruction wherever the squared-window sum is positive
+    (the division by sum w^2 makes any hop <= n_fft invertible)."""
+    x = rnd(2, L)
+    w = oracle.hann_window(n_fft)
+    for normalized in (False, True):
+        y = oracle.istft(oracle.stft(x, n_fft, hop, w, center, normalized), n_fft, hop, w,
+                         length=L, center=center, normalized=normalized)
+        # covered span: the first sample has w[0] = 0 without centring; the
+        # frames end at (T - 1) hop + n_fft (minus the centre padding), and
+        # the rest of `length` is zero-padded, as torch.istft does
+        lo = 0 if center else 1
+        T = (L + (n_fft if center else 0) - n_fft) // hop + 1
+        hi = min(L, (T - 1) * hop + n_fft - (n_fft if center else 1))
+        # near the uncentred edges sum w^2 is tiny (w[1]^2 ~ 1e-5 at n_fft 64)
+        # and the division magnifies the fp32 rounding of the spectrum: compare
+        # where sum w^2 > 1e-2
+        ws = np.zeros(L + n_fft)
+        pad = n_fft // 2 if center else 0
+        for t in range(T):
+            ws[t * hop:t * hop + n_fft] += w.astype(np.float64) ** 2
+        ok = np.nonzero(ws[pad:pad + L] > 1e-2)[0]
+        ok = ok[(ok >= lo) & (ok < hi)]
+        assert len(ok) > 0.9 * (hi - lo)
+        assert rel_err(y[:, ok], x[:, ok]) < 1e-6
+        tail = hi if center else hi + 1
+        assert np.all(y[:, tail:] == 0)
+
+
+def test_istft_ignores_dc_and_nyquist_imaginary_parts_and_pads(oracle):
+    n_fft, hop = 32, 8
+    spec = rnd(1, n_fft // 2 + 1, 6, 2)
+    w = oracle.hann_window(n_fft)
+    a = oracle.istft(spec, n_fft, hop, w)
+    s2 = spec.copy()
+    s2[:, 0, :, 1] = 5.0
+    s2[:, -1, :, 1] = -3.0
+    np.testing.assert_array_equal(oracle.istft(s2, n_fft, hop, w), a)
+    longer = oracle.istft(spec, n_fft, hop, w, length=a.shape[1] + 7)
+    np.testing.assert_array_equal(longer[:, :a.shape[1]], a)
+    assert np.all(longer[:, a.shape[1]:] == 0)
+    np.testing.assert_array_equal(oracle.istft(spec, n_fft, hop, w, length=10), a[:, :10])
+    # float64 irfft restatement of one frame's contribution
+    X = spec[0, :, :, 0].astype(np.float64) + 1j * spec[0, :, :, 1]
+    X[0].imag = 0
+    X[-1].imag = 0
+    fr = np.fft.irfft(X.T, n=n_fft, axis=-1) * w                      # [T, n_fft]
+    full = np.zeros(n_fft + 5 * hop)
+    ws = np.zeros_like(full)
+    for t in range(6):
+        full[t * hop:t * hop + n_fft] += fr[t]
+        ws[t * hop:t * hop + n_fft] += w.astype(np.float64) ** 2
+    full = np.where(ws > 1e-8, full / np.where(ws > 1e-8, ws, 1), full)
+    assert rel_err(a[0], full[n_fft // 2:-(n_fft // 2)]) < 1e-6
