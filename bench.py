@@ -289,6 +289,9 @@ def band_table(msst, torch, B):
     feats = plan.band_split(x)
     m = plan.mask_estimator(feats)
     masks = m.reshape(1, B, FRAMES, ftot)
+    # 8 s of stereo audio at 44.1 kHz -> 801 frames (n_fft 2048, hop 441)
+    audio = torch.randn(2 * B, (FRAMES - 1) * 441, device="cuda", generator=gen)
+    win = msst.hann_window(2048)
     out = {}
     f_split = 2.0 * rows * ftot * DIM
     f_mask = 2.0 * rows * nb * DIM * hid + 2.0 * rows * hid * 2 * ftot
@@ -298,7 +301,11 @@ def band_table(msst, torch, B):
             ("mask_estimator", lambda: plan.mask_estimator(feats, out=m), f_mask,
              4 * rows * nb * DIM + 4 * rows * ftot + 2 * nb * hid * (DIM + 2 * 2 * ftot // nb)),
             ("band_gather", lambda: plan.band_gather(stft, B), 0, 8 * rows * ftot),
-            ("mask_merge", lambda: plan.mask_merge(masks, stft, B), 0, 12 * rows * ftot)):
+            ("mask_merge", lambda: plan.mask_merge(masks, stft, B), 0, 12 * rows * ftot),
+            ("stft", lambda: msst.stft(audio, 2048, 441, win), 0,
+             4 * audio.numel() + 8 * 2 * B * 1025 * FRAMES),
+            ("istft", lambda: msst.istft(stft, 2048, 441, win, length=audio.shape[1]), 0,
+             8 * 2 * B * 1025 * FRAMES + 4 * audio.numel())):
         fn()
         us = time_events(torch, fn, 50) / 50 * 1e3
         e = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
@@ -308,7 +315,8 @@ def band_table(msst, torch, B):
         out[name] = e
     out["config"] = f"BSRoformer bands: 62 bands, features {ftot}, rows {rows}, dim {DIM}, " \
                     f"MLP {DIM}->{hid}->2*band, fp16 weights, fp32 input; STFT side: " \
-                    f"stereo, 1025 bins, {FRAMES} frames, one stem"
+                    f"stereo, 1025 bins, {FRAMES} frames, one stem; STFT / iSTFT of 8 s " \
+                    f"stereo at 44.1 kHz, n_fft 2048, hop 441, fp32"
     return out
 
 

@@ -357,6 +357,33 @@ static void test_bands() {
     }
 }
 
+static void test_stft() {
+    // ops::stft / istft / hann_window (ops.h:87-96) against the oracle.
+    const int n_fft = 256, hop = 64;
+    const int64_t B = 2, L = 3000;
+    Tensor w = ops::hann_window(n_fft);
+    std::vector<float> wr(n_fft);
+    orc_hann_window(wr.data(), n_fft);
+    check_close("hann_window", w, wr, 1e-6);
+    auto x = randn((size_t)(B * L), 1.0f, 61);
+    Tensor s = ops::stft(dev(x, {B, L}, DType::Float32), n_fft, hop, n_fft, w);
+    const int64_t T = (L + n_fft - n_fft) / hop + 1, F = n_fft / 2 + 1;
+    expect(s.shape() == std::vector<int64_t>({B, F, T, 2}), "stft -> [B, F, T, 2]");
+    std::vector<float> rs((size_t)(B * F * T * 2));
+    orc_stft(x.data(), B, L, n_fft, hop, wr.data(), 1, 0, rs.data());
+    check_close("stft", s, rs, 1e-5);
+    Tensor y = ops::istft(s, n_fft, hop, n_fft, w, L);
+    expect(y.shape() == std::vector<int64_t>({B, L}), "istft -> [B, length]");
+    std::vector<float> ry((size_t)(B * L));
+    const std::vector<float> sh = s.to_cpu_f32();
+    orc_istft(sh.data(), B, T, n_fft, hop, wr.data(), L, 1, 0, ry.data());
+    check_close("istft", y, ry, 1e-5);
+    Tensor s1 = ops::stft(dev(x, {L}, DType::Float32), n_fft, hop, n_fft, w);  // 1-D signal
+    expect(s1.shape() == std::vector<int64_t>({1, F, T, 2}), "stft of [L] -> [1, F, T, 2]");
+    expect_throw("stft with win_length != n_fft",
+                 [&] { ops::stft(dev(x, {B, L}, DType::Float32), n_fft, hop, 200, w); });
+}
+
 int main() {
     try {
         test_tensor();
@@ -365,6 +392,7 @@ int main() {
         test_rope_attention();
         test_stack();
         test_bands();
+        test_stft();
         cudasep::CudaContext::instance().sync();
     } catch (const std::exception& ex) {
         std::printf("FAIL: uncaught exception: %s\n", ex.what());

@@ -25,6 +25,9 @@ SIGNATURES = [
     "cudasep::ops::rms_norm(cudasep::Tensor const&, cudasep::Tensor const&, float)",
     "cudasep::ops::apply_rotary_emb(cudasep::Tensor&, cudasep::Tensor&, cudasep::Tensor const&, cudasep::Tensor const&)",
     "cudasep::ops::scaled_dot_product_attention(cudasep::Tensor const&, cudasep::Tensor const&, cudasep::Tensor const&, float, float)",
+    "cudasep::ops::stft(cudasep::Tensor const&, int, int, int, cudasep::Tensor const&, bool, bool)",
+    "cudasep::ops::istft(cudasep::Tensor const&, int, int, int, cudasep::Tensor const&, long, bool, bool)",
+    "cudasep::ops::hann_window(int)",
     "cudasep::ops::tanh_act(cudasep::Tensor const&)",
     "cudasep::ops::glu(cudasep::Tensor const&, int)",
     "cudasep::ops::BandPlan::band_split(cudasep::Tensor const&) const",
