@@ -103,6 +103,9 @@ _SIGS = {
     "msst_band_gather": ([_BCP, _vp, _vp, _i64, _i64, _vp, _vp], _int),
     "msst_mask_merge_workspace": ([_BCP, _i64, _i64, _i64], _i64),
     "msst_mask_merge": ([_BCP, _vp, _vp, _i64, _vp, _i64, _i64, _int, _vp, _vp, _i64, _vp], _int),
+    "msst_chunk_extract": ([_vp, _i64, _i64, _i64, _i64, _i64, _int, _vp, _vp], _int),
+    "msst_overlap_add": ([_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp], _int),
+    "msst_normalize_by_weights": ([_vp, _vp, _i64, _i64, _vp], _int),
     "msst_stft_frames": ([_i64, _int, _int, _int], _i64),
     "msst_stft": ([_vp, _i64, _i64, _int, _int, _vp, _int, _int, _vp, _vp], _int),
     "msst_istft_length": ([_i64, _int, _int, _i64, _int], _i64),

@@ -9,11 +9,20 @@
 //   msst_tanh              elementwise tanh (ops_elementwise.cu:84-88, :138)
 //   msst_glu               last-axis GLU, first half * sigmoid(second half)
 //                          (ops_elementwise.cu:321-388)
+//   msst_chunk_extract     one chunk of the chunked driver: the audio seen
+//                          through its border reflect padding, with the last
+//                          chunk reflect- or zero-padded (inference_app.cpp:
+//                          116-156)
+//   msst_overlap_add       out += chunk * fade, weights += fade
+//                          (ops_fused.cu:138-168; in stream order, no atomics)
+//   msst_normalize_by_weights  out /= weights where > 1e-8 (ops_fused.cu:170-186)
 //   msst_swap_axes12       [A,P,Q,R] -> [A,Q,P,R], the permute({0,2,1,3})
 //                          .contiguous() of the depth loop
 //                          (model_bs_roformer.cu:491, :509; tensor.cu:868-903)
 // The fused Roformer stack does not use the first two: its attention kernel
 // reads the packed qkv rows and writes merged, gated rows directly.
+#include <algorithm>
+
 #include "msst_common.hpp"
 
 namespace msst {
@@ -102,6 +111,61 @@ __global__ __launch_bounds__(256) void glu_kernel(const T* __restrict__ x, T* __
         const float a = (float)x[r * 2 * half + j], g = (float)x[r * 2 * half + half + j];
         out[i] = (T)(a * (1.0f / (1.0f + expf(-g))));
     }
+}
+
+// Reflect index into [0, n) (edge sample not repeated; |p| < n).
+__device__ __forceinline__ int64_t reflect_index(int64_t p, int64_t n) {
+    if (p < 0) p = -p;
+    if (p >= n) p = 2 * (n - 1) - p;
+    return p;
+}
+
+// dst[c, i] for i < chunk: P[start + i] where P = audio reflect-padded by
+// `border` on both sides; past the end of P, the chunk's own slice
+// reflect-padded at its end (tail_reflect) or zero.
+__global__ __launch_bounds__(256) void chunk_extract_kernel(const float* __restrict__ audio,
+                                                            int64_t length, int64_t border,
+                                                            int64_t start, int64_t chunk,
+                                                            int tail_reflect,
+                                                            float* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t c = blockIdx.y;
+    if (i >= chunk) return;
+    const int64_t plen = length + 2 * border;
+    const int64_t actual = min(chunk, plen - start);
+    float v = 0.0f;
+    int64_t q = -1;
+    if (i < actual)
+        q = start + i;
+    else if (tail_reflect)
+        q = start + (2 * actual - 2 - i);
+    if (q >= 0) v = audio[c * length + reflect_index(q - border, length)];
+    dst[c * chunk + i] = v;
+}
+
+__global__ __launch_bounds__(256) void overlap_add_kernel(float* __restrict__ out,
+                                                          float* __restrict__ wsum,
+                                                          const float* __restrict__ src,
+                                                          int64_t src_stride,
+                                                          const float* __restrict__ window,
+                                                          int64_t total, int64_t offset,
+                                                          int64_t len) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t c = blockIdx.y;
+    if (i >= len) return;
+    const float w = window[i];
+    out[c * total + offset + i] += src[c * src_stride + i] * w;
+    if (c == 0) wsum[offset + i] += w;
+}
+
+__global__ __launch_bounds__(256) void normalize_by_weights_kernel(float* __restrict__ out,
+                                                                   const float* __restrict__ wsum,
+                                                                   int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t c = blockIdx.y;
+    if (i >= total) return;
+    const float w = wsum[i];
+    if (w > 1e-8f) out[c * total + i] /= w;
 }
 
 // [A,P,Q,R] -> [A,Q,P,R]; one thread per 16-byte (or element) chunk of R.
@@ -293,4 +357,51 @@ extern "C" int msst_swap_axes12(const void* src, void* dst, int dtype, int64_t A
                            Q, R);
     }
     return check_launch("swap12_kernel");
+}
+
+extern "C" int msst_chunk_extract(const float* audio, int64_t channels, int64_t length,
+                                  int64_t border, int64_t start, int64_t chunk, int tail_reflect,
+                                  float* dst, void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(audio && dst, MSST_ERR_INVALID_ARG, "null pointer");
+    MSST_REQUIRE(channels >= 1 && channels < 65536 && length >= 1 && chunk >= 1 && border >= 0,
+                 MSST_ERR_INVALID_ARG, "bad shape");
+    MSST_REQUIRE(border < length, MSST_ERR_INVALID_ARG, "border reflect padding needs border < length");
+    const int64_t plen = length + 2 * border;
+    MSST_REQUIRE(start >= 0 && start < plen, MSST_ERR_INVALID_ARG, "chunk start out of range");
+    const int64_t actual = std::min(chunk, plen - start);
+    MSST_REQUIRE(!tail_reflect || actual == chunk || 2 * actual > chunk, MSST_ERR_INVALID_ARG,
+                 "tail reflect padding needs more than half a chunk of signal");
+    const dim3 grid((unsigned)((chunk + 255) / 256), (unsigned)channels);
+    hipLaunchKernelGGL(chunk_extract_kernel, grid, dim3(256), 0, as_stream(stream), audio, length,
+                       border, start, chunk, tail_reflect, dst);
+    return check_launch("chunk_extract_kernel");
+}
+
+extern "C" int msst_overlap_add(float* out, float* wsum, const float* src, int64_t src_stride,
+                                const float* window, int64_t channels, int64_t total,
+                                int64_t offset, int64_t len, void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(out && wsum && src && window, MSST_ERR_INVALID_ARG, "null pointer");
+    MSST_REQUIRE(channels >= 1 && channels < 65536 && len >= 0 && offset >= 0 &&
+                     offset + len <= total && src_stride >= len,
+                 MSST_ERR_INVALID_ARG, "bad shape");
+    if (len == 0) return MSST_OK;
+    const dim3 grid((unsigned)((len + 255) / 256), (unsigned)channels);
+    hipLaunchKernelGGL(overlap_add_kernel, grid, dim3(256), 0, as_stream(stream), out, wsum, src,
+                       src_stride, window, total, offset, len);
+    return check_launch("overlap_add_kernel");
+}
+
+extern "C" int msst_normalize_by_weights(float* out, const float* wsum, int64_t channels,
+                                         int64_t total, void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(out && wsum, MSST_ERR_INVALID_ARG, "null pointer");
+    MSST_REQUIRE(channels >= 1 && channels < 65536 && total >= 0, MSST_ERR_INVALID_ARG,
+                 "bad shape");
+    if (total == 0) return MSST_OK;
+    const dim3 grid((unsigned)((total + 255) / 256), (unsigned)channels);
+    hipLaunchKernelGGL(normalize_by_weights_kernel, grid, dim3(256), 0, as_stream(stream), out,
+                       wsum, total);
+    return check_launch("normalize_by_weights_kernel");
 }

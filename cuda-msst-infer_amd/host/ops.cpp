@@ -325,9 +325,15 @@ BandPlan::BandPlan(std::vector<int> band_dims, int dim, const BandSplitWeights* 
         keep_.push_back(t.to_f32());
         return keep_.back().data_f32();
     };
+    // fp32 matrices select the per-band fp32 path (all matrices one dtype).
+    const Tensor* first = split && !split->w.empty() ? &split->w[0]
+                          : mask && !mask->w.empty() && !mask->w[0].empty() ? &mask->w[0][0]
+                                                                              : nullptr;
+    fp32_ = first && first->dtype() == DType::Float32;
+    const DType mdt = fp32_ ? DType::Float32 : DType::Float16;
     auto f16w = [&](const Tensor& t) -> const void* {
-        if (t.dtype() != DType::Float16)
-            throw std::runtime_error("BandPlan: band weights must be fp16 (g_quantize_fp16)");
+        if (t.dtype() != mdt)
+            throw std::runtime_error("BandPlan: band matrices must all be fp16 or all fp32");
         return t.data_ptr();
     };
     std::vector<const float*> sg, sb, mb;
@@ -365,11 +371,32 @@ BandPlan::BandPlan(std::vector<int> band_dims, int dim, const BandSplitWeights* 
             }
         }
     }
+    if (fp32_) {
+        // The plan keeps only the STFT side; the matrices stay with the ops.
+        if (split) split32_ = *split;
+        if (mask) mask32_ = *mask;
+        check(msst_band_plan_init(&c, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                  plan_.data_ptr(), bytes, stream()),
+              "BandPlan");
+        return;
+    }
     check(msst_band_plan_init(&c, split ? sg.data() : nullptr, split ? sw.data() : nullptr,
                               split ? sb.data() : nullptr, mask ? mw.data() : nullptr,
                               mask ? mb.data() : nullptr, plan_.data_ptr(), bytes, stream()),
           "BandPlan");
 }
+
+namespace {
+// dst[r, 0..cols) = src[r * src_pitch + 0..cols) (elements of `bytes_per`).
+void copy2d(void* dst, int64_t dst_pitch, const void* src, int64_t src_pitch, int64_t cols,
+            int64_t rows, size_t bytes_per) {
+    if (rows == 0 || cols == 0) return;
+    HIP_CHECK(hipMemcpy2DAsync(dst, (size_t)dst_pitch * bytes_per, src,
+                               (size_t)src_pitch * bytes_per, (size_t)cols * bytes_per,
+                               (size_t)rows, hipMemcpyDeviceToDevice,
+                               reinterpret_cast<hipStream_t>(stream())));
+}
+}  // namespace
 
 Tensor BandPlan::band_gather(const Tensor& stft, int64_t batch) const {
     if (stft_.channels == 0) throw std::runtime_error("band_gather: plan has no STFT side");
@@ -421,6 +448,22 @@ Tensor BandPlan::band_split(const Tensor& x) const {
     shape.back() = (int64_t)dims_.size();
     shape.push_back(dim_);
     Tensor out = Tensor::empty(shape, DType::Float32);
+    if (fp32_) {
+        // model_bs_roformer.cu:337-368, band by band on the fp32 ops.
+        if (split32_.w.empty()) throw std::runtime_error("band_split: plan has no split weights");
+        const int64_t nb = (int64_t)dims_.size();
+        int64_t off = 0;
+        for (int64_t b = 0; b < nb; ++b) {
+            const int64_t d = dims_[b];
+            Tensor xb = Tensor::empty({rows, d});
+            copy2d(xb.data_ptr(), d, x.data_f32() + off, ftot, d, rows, 4);
+            Tensor o = linear(rms_norm(xb, split32_.gamma[b], std::sqrt((float)d)), split32_.w[b],
+                              split32_.b[b]);
+            copy2d(out.data_f32() + b * dim_, nb * dim_, o.data_ptr(), dim_, dim_, rows, 4);
+            off += d;
+        }
+        return out;
+    }
     const msst_band_config c = config();
     const int64_t wsb = msst_band_split_workspace(&c, rows);
     Tensor ws = Tensor::empty({std::max<int64_t>((wsb + 3) / 4, 1)}, DType::Float32);
@@ -440,6 +483,25 @@ Tensor BandPlan::mask_estimator(const Tensor& x) const {
     std::vector<int64_t> shape(x.shape().begin(), x.shape().end() - 2);
     shape.push_back(ftot);
     Tensor out = Tensor::empty(shape, DType::Float32);
+    if (fp32_) {
+        // model_bs_roformer.cu:374-414, band by band on the fp32 ops.
+        if (mask32_.w.empty()) throw std::runtime_error("mask_estimator: plan has no MLP weights");
+        Tensor xf = x.to_f32();
+        int64_t off = 0;
+        for (int64_t b = 0; b < nb; ++b) {
+            Tensor h = Tensor::empty({rows, (int64_t)dim_});
+            copy2d(h.data_ptr(), dim_, xf.data_f32() + b * dim_, nb * dim_, dim_, rows, 4);
+            for (int l = 0; l < linears_; ++l) {
+                h = linear(h, mask32_.w[b][l], mask32_.b[b][l]);
+                if (l < linears_ - 1) h = tanh_act(h);
+            }
+            Tensor g = glu(h, -1);
+            const int64_t d = dims_[b];
+            copy2d(out.data_f32() + off, ftot, g.data_ptr(), d, d, rows, 4);
+            off += d;
+        }
+        return out;
+    }
     const msst_band_config c = config();
     const int64_t wsb = msst_mask_estimator_workspace(&c, rows);
     Tensor ws = Tensor::empty({std::max<int64_t>((wsb + 3) / 4, 1)}, DType::Float32);

@@ -117,8 +117,10 @@ void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int hea
 // band_freq_dims_).  Weights per band as the models hold them
 // (model_bs_roformer.h:65-70, :105-115): gamma [fd] and W [dim, fd], b [dim]
 // for the split; w[b][l] / bias[b][l] for the L linears of band b's MLP.
-// Matrices must be fp16 (the reference's fp16 mode converts them at load,
-// weights.cu:510-524); gammas and biases may be fp16 or fp32.
+// fp16 matrices run the grouped kernels (bands.hip); fp32 matrices (the
+// reference's fp32 mode) run the reference's per-band loop on the fp32 ops
+// (rms_norm, linear, tanh_act, glu), one band at a time.  Gammas and biases
+// may be fp16 or fp32.
 struct BandSplitWeights {
     std::vector<Tensor> gamma, w, b;
 };
@@ -160,6 +162,9 @@ private:
     std::vector<int> dims_;
     int dim_ = 0, hidden_ = 0, linears_ = 1;
     StftBands stft_;
+    bool fp32_ = false;                 // per-band fp32 path
+    BandSplitWeights split32_;          // fp32 path: the caller's tensors
+    MaskEstimatorWeights mask32_;
     Tensor plan_;
     std::vector<Tensor> keep_;  // fp32 copies of fp16 gammas / biases
     msst_band_config config() const;

@@ -36,6 +36,11 @@
  *   msst_stft                   ops.h:87-89   (ops_stft.cu:286-362, cuFFT R2C)
  *   msst_istft                  ops.h:91-93   (ops_stft.cu:368-491, cuFFT C2R)
  *   msst_hann_window            ops.h:96      (ops_stft.cu:268-280)
+ *   msst_chunk_extract          inference_app.cpp:116-156 (pad_reflect of the mix,
+ *                               slice, pad_reflect / pad of the last chunk)
+ *   msst_overlap_add            ops_fused.cu:138-168 (fused_overlap_add_kernel +
+ *                               fused_weight_add_kernel)
+ *   msst_normalize_by_weights   ops_fused.cu:170-186
  *   msst_band_plan_init         the per-band weight tables of
  *                               model_bs_roformer.h:65-70, :105-115
  *   msst_rms_norm               ops.h:56               (ops_norm.cu:455-491)
@@ -334,6 +339,25 @@ int64_t msst_mask_merge_workspace(const msst_band_config* c, int64_t batch, int6
 int msst_mask_merge(const msst_band_config* c, const void* plan, const float* masks,
                     int64_t stems, const float* stft, int64_t batch, int64_t frames,
                     int zero_dc, float* out, void* workspace, int64_t ws_bytes, void* stream);
+
+/* ---- Chunked inference (inference_app.cpp:100-324) --------------------------
+ * dst [channels, chunk] = samples [start, start + chunk) of the audio
+ * [channels, length] reflect-padded by `border` on both sides (border <
+ * length); past its end, the chunk's own slice reflect-padded at its end
+ * (tail_reflect; needs more than half a chunk of signal) or zero. */
+int msst_chunk_extract(const float* audio, int64_t channels, int64_t length, int64_t border,
+                       int64_t start, int64_t chunk, int tail_reflect, float* dst, void* stream);
+
+/* out[c, offset + i] += src[c * src_stride + i] * window[i] and
+ * wsum[offset + i] += window[i] for i < len; out [channels, total].  Calls
+ * on one stream apply in order (no atomics: run to run identical). */
+int msst_overlap_add(float* out, float* wsum, const float* src, int64_t src_stride,
+                     const float* window, int64_t channels, int64_t total, int64_t offset,
+                     int64_t len, void* stream);
+
+/* out[c, i] /= wsum[i] where wsum[i] > 1e-8. */
+int msst_normalize_by_weights(float* out, const float* wsum, int64_t channels, int64_t total,
+                              void* stream);
 
 /* ---- STFT / iSTFT (torch.stft / torch.istft semantics, as the reference) --
  * Hand-written FFT (power-of-two n_fft in [16, 4096]); the window has n_fft

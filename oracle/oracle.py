@@ -325,3 +325,101 @@ def istft(spec, n_fft, hop, window, length=-1, center=True, normalized=False) ->
     lib().orc_istft(_p(s), B, T, n_fft, hop, _p(w), out_len, int(center), int(normalized),
                     _p(out))
     return out
+
+
+# ------------------------------------------------------------------ BSRoformer
+def bsroformer_forward(cfg: dict, w: dict, audio) -> np.ndarray:
+    """BSRoformer::forward (model_bs_roformer.cu:420-609) composed from the
+    functions above.  cfg: the checkpoint config; w: name -> fp32 array (the
+    reference's weight names); audio [B, ch, S] -> [B, stems, ch, S']."""
+    audio = _f32(audio)
+    B, ch, S = audio.shape
+    n_fft, hop = cfg.get("stft_n_fft", 2048), cfg.get("stft_hop_length", 441)
+    norm = bool(cfg.get("stft_normalized", False))
+    stems, depth = cfg.get("num_stems", 1), cfg.get("depth", 12)
+    L = cfg.get("mask_estimator_depth", 1)
+    fpb = cfg["freqs_per_bands"]
+    dims = [2 * f * ch for f in fpb]
+    win = hann_window(n_fft)
+    spec = stft(audio.reshape(B * ch, S), n_fft, hop, win, True, norm)      # [B*ch, F, T, 2]
+    x = band_gather(spec, B)
+    nb = len(dims)
+    feats = band_split(
+        x.reshape(-1, x.shape[-1]), dims,
+        [w[f"band_split.to_features.{b}.0.gamma"] for b in range(nb)],
+        [w[f"band_split.to_features.{b}.1.weight"] for b in range(nb)],
+        [w[f"band_split.to_features.{b}.1.bias"] for b in range(nb)])
+    T = spec.shape[2]
+    feats = feats.reshape(B, T, nb, -1)
+    layers = []
+    for d in range(depth):
+        for t in range(2):
+            p = f"layers.{d}.{t}.layers.0"
+            layers.append(LayerWeights(
+                w[p + ".0.norm.gamma"], w[p + ".0.to_qkv.weight"], w[p + ".0.to_gates.weight"],
+                w[p + ".0.to_gates.bias"], w[p + ".0.to_out.0.weight"], w[p + ".1.net.0.gamma"],
+                w[p + ".1.net.1.weight"], w[p + ".1.net.1.bias"], w[p + ".1.net.4.weight"],
+                w[p + ".1.net.4.bias"]))
+    feats = roformer_stack(feats, layers, cfg.get("heads", 8), cfg.get("dim_head", 64),
+                           w["final_norm.gamma"])
+    masks = []
+    for s in range(stems):
+        ws = [[w[f"mask_estimators.{s}.to_freqs.{b}.0.{2 * i}.weight"] for i in range(L)]
+              for b in range(nb)]
+        bs = [[w[f"mask_estimators.{s}.to_freqs.{b}.0.{2 * i}.bias"] for i in range(L)]
+              for b in range(nb)]
+        masks.append(mask_estimator(feats.reshape(B * T, nb, -1), dims, ws, bs).reshape(B, T, -1))
+    merged = mask_merge(np.stack(masks), spec, B, None, bool(cfg.get("zero_dc", True)))
+    length = S if cfg.get("match_input_audio_length", False) else -1
+    y = istft(merged, n_fft, hop, win, length, True, norm)
+    return y.reshape(B, stems, ch, -1)
+
+
+def process_chunked(audio, chunk_size: int, step: int, batch: int, forward) -> np.ndarray:
+    """The chunked driver (inference_app.cpp:100-324, Generic mode) in numpy:
+    audio [ch, S]; forward maps [b, ch, chunk] -> [b, ..., n]."""
+    audio = _f32(audio)
+    C, S = audio.shape
+    fade_size = chunk_size // 10
+    border = chunk_size - step
+    mix = audio
+    padded = S > 2 * border and border > 0
+    if padded:
+        mix = np.pad(audio, ((0, 0), (border, border)), mode="reflect")
+    total = mix.shape[1]
+    starts = list(range(0, total, step))
+    fade = np.ones(chunk_size, np.float32)
+    if fade_size == 1:
+        fade[0] = fade[-1] = 0.0
+    elif fade_size > 1:
+        a = (np.arange(fade_size) / (fade_size - 1)).astype(np.float32)
+        fade[:fade_size] = a
+        fade[-fade_size:] = 1.0 - a
+    out, wsum = None, np.zeros(total, np.float32)
+    for g in range(0, len(starts), max(1, min(batch, len(starts)))):
+        group = starts[g:g + batch]
+        chunks = []
+        for st in group:
+            c = mix[:, st:st + chunk_size]
+            actual = c.shape[1]
+            if actual < chunk_size:
+                mode = "reflect" if actual > chunk_size // 2 else "constant"
+                c = np.pad(c, ((0, 0), (0, chunk_size - actual)), mode=mode)
+            chunks.append(c)
+        y = forward(np.stack(chunks))
+        n = y.shape[-1]
+        y = y.reshape(len(group), -1, n)
+        if out is None:
+            out = np.zeros((y.shape[1], total), np.float32)
+        for l, st in enumerate(group):
+            actual = min(chunk_size, total - st)
+            wnd = fade.copy()
+            if fade_size > 0 and st == 0:
+                wnd[:fade_size] = 1.0
+            if fade_size > 0 and st + chunk_size >= total:
+                wnd[-fade_size:] = 1.0
+            m = min(actual, n)
+            out[:, st:st + m] += y[l, :, :m] * wnd[:m]
+            wsum[st:st + m] += wnd[:m]
+    out = np.where(wsum > 1e-8, out / np.where(wsum > 1e-8, wsum, 1.0), out)
+    return out[:, border:border + S] if padded else out

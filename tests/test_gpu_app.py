@@ -1,0 +1,111 @@
+"""End to end through the msst_infer CLI (the reference's cudasep_infer file
+path): a synthetic BSRoformer .csm (random weights under the reference's
+names), a stereo WAV in, float WAVs out, compared with the oracle's
+BSRoformer forward run through the oracle's chunked driver.
+
+Config: dim 128, depth 1, 2 heads, 2 stems, 19 bands over a 256-point STFT
+(hop 64), mask-estimator MLP of 2 linears, chunk 4096 with 2 overlaps, so a
+10000-sample track takes the chunked path (border reflect padding, batch 2,
+a zero-padded last chunk) and a 3000-sample one the direct path.
+Tolerances: fp32 (--fp32) 1e-4, fp16 weights (--fp16) 2e-2, normwise per stem.
+"""
+from __future__ import annotations
+
+import copy
+import os
+import subprocess
+
+import numpy as np
+import pytest
+from scipy.io import wavfile
+
+import csm_file
+from conftest import ROOT, TOL_F16, rel_err
+
+pytestmark = pytest.mark.gpu
+
+CLI = os.path.join(ROOT, "cuda-msst-infer_amd", "msst_infer")
+
+CFG = {"model_type": "bs_roformer", "dim": 128, "depth": 1, "heads": 2, "dim_head": 64,
+       "stereo": True, "num_stems": 2, "mask_estimator_depth": 2, "mlp_expansion_factor": 4,
+       "zero_dc": True, "stft_n_fft": 256, "stft_hop_length": 64, "stft_win_length": 256,
+       "freqs_per_bands": [4] * 8 + [8] * 8 + [16] * 2 + [1], "chunk_size": 4096,
+       "num_overlap": 2, "sample_rate": 44100, "instruments": ["vocals", "other"]}
+
+
+def run_cli(args):
+    print("running", " ".join(args), flush=True)
+    r = subprocess.run([CLI] + args, capture_output=True, text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0, r.stderr
+    return r.stdout
+
+
+def separate(tmp_path, cfg, w, audio, mode):
+    model = tmp_path / "m.csm"
+    csm_file.write_csm(model, cfg, w)
+    inp = tmp_path / "mix.wav"
+    wavfile.write(inp, cfg["sample_rate"], np.ascontiguousarray(audio.T))
+    out = tmp_path / f"out_{mode}"
+    run_cli(["--model", str(model), "--input", str(inp), "--output", str(out), "--stem", "-1",
+             f"--{mode}"])
+    stems = []
+    for name in cfg["instruments"]:
+        sr, y = wavfile.read(out / f"{name}.wav")
+        assert sr == cfg["sample_rate"] and y.dtype == np.float32
+        stems.append(y.T)
+    return np.stack(stems)  # [stems, ch, S]
+
+
+def oracle_separate(oracle, cfg, w, audio):
+    chunk = cfg["chunk_size"]
+    step = chunk // cfg["num_overlap"]
+    fwd = lambda b: oracle.bsroformer_forward(cfg, w, b)
+    if audio.shape[1] > chunk:
+        y = oracle.process_chunked(audio, chunk, step, 2, fwd)
+        return y.reshape(cfg["num_stems"], audio.shape[0], -1)
+    return fwd(audio[None])[0]
+
+
+@pytest.mark.parametrize("S", [10000, 3000])
+@pytest.mark.parametrize("mode", ["fp32", "fp16"])
+def test_cli_matches_oracle(tmp_path, oracle, cuda, S, mode):
+    rng = np.random.default_rng(S)
+    audio = (0.3 * rng.standard_normal((2, S))).astype(np.float32)
+    w = csm_file.bsr_checkpoint(CFG, seed=2)
+    y = separate(tmp_path, CFG, w, audio, mode)
+    wr = {k: (v.astype(np.float16).astype(np.float32) if (mode == "fp16" and v.ndim == 2) else v)
+          for k, v in w.items()}
+    r = oracle_separate(oracle, CFG, wr, audio)
+    assert y.shape == r.shape
+    tol = 1e-4 if mode == "fp32" else TOL_F16
+    for s in range(y.shape[0]):
+        assert rel_err(y[s], r[s]) < tol, (s, rel_err(y[s], r[s]))
+
+
+def test_cli_unit_mask_returns_the_mix(tmp_path, cuda):
+    """Masks of 1 + 0i with zero_dc off: every stem is the mix itself
+    (STFT -> iSTFT, band gather / merge, chunk stitching), independent of
+    the oracle."""
+    cfg = copy.deepcopy(CFG)
+    cfg["zero_dc"] = False
+    w = csm_file.bsr_checkpoint(cfg, seed=3, unit_mask=True)
+    audio = (0.5 * np.random.default_rng(9).standard_normal((2, 10000))).astype(np.float32)
+    y = separate(tmp_path, cfg, w, audio, "fp16")
+    for s in range(y.shape[0]):
+        assert rel_err(y[s], audio) < 1e-5
+
+
+def test_cli_list_stems_and_errors(tmp_path, cuda):
+    model = tmp_path / "m.csm"
+    csm_file.write_csm(model, CFG, csm_file.bsr_checkpoint(CFG, seed=4))
+    out = run_cli(["--model", str(model), "--list-stems"])
+    assert "[0] vocals" in out and "[1] other" in out
+    r = subprocess.run([CLI, "--model", str(tmp_path / "missing.csm"), "--input", "x.wav"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 1 and "cannot open" in r.stderr
+    bad = tmp_path / "bad.csm"
+    bad.write_bytes(b"XXXX" + bytes(12))
+    r = subprocess.run([CLI, "--model", str(bad), "--list-stems"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 1 and "magic" in r.stderr

@@ -508,3 +508,35 @@ def test_istft_ignores_dc_and_nyquist_imaginary_parts_and_pads(oracle):
         ws[t * hop:t * hop + n_fft] += w.astype(np.float64) ** 2
     full = np.where(ws > 1e-8, full / np.where(ws > 1e-8, ws, 1), full)
     assert rel_err(a[0], full[n_fft // 2:-(n_fft // 2)]) < 1e-6
+
+
+# ------------------------------------------------- model composition and driver
+SMALL_BSR = {"model_type": "bs_roformer", "dim": 128, "depth": 1, "heads": 2, "dim_head": 64,
+             "stereo": True, "num_stems": 2, "mask_estimator_depth": 2, "mlp_expansion_factor": 4,
+             "zero_dc": False, "stft_n_fft": 256, "stft_hop_length": 64, "stft_win_length": 256,
+             "freqs_per_bands": [4] * 8 + [8] * 8 + [16] * 2 + [1], "chunk_size": 4096,
+             "num_overlap": 2, "sample_rate": 44100}
+
+
+def test_process_chunked_identity_model_returns_input(oracle):
+    """With a model that returns its input, the fades and the weight
+    normalisation cancel: the driver returns the track itself (border
+    reflect padding, the reflect / zero-padded last chunk and batching
+    included)."""
+    for S in (10000, 4096 * 3 + 17, 5000):
+        x = rnd(2, S)
+        y = oracle.process_chunked(x, 4096, 2048, 2, lambda b: b)
+        np.testing.assert_allclose(y, x, rtol=1e-6, atol=1e-6)
+
+
+def test_bsroformer_forward_unit_mask_returns_input(oracle):
+    """A checkpoint whose mask estimators output 1 + 0i leaves the STFT
+    untouched: the forward is istft(stft(x)) = x (zero_dc off), which pins
+    the layout hand-offs of the composition (gather, merge, stereo split)."""
+    import csm_file
+    w = csm_file.bsr_checkpoint(SMALL_BSR, seed=1, unit_mask=True)
+    x = rnd(1, 2, 64 * 40)
+    y = oracle.bsroformer_forward(SMALL_BSR, w, x)
+    assert y.shape == (1, 2, 2, 64 * 40)
+    for s in range(2):
+        assert rel_err(y[0, s], x[0]) < 1e-5
