@@ -1,6 +1,7 @@
-// msst_infer — separate a WAV file with a BSRoformer .csm checkpoint on one
-// MI355X (the file-inference surface of the reference's cudasep_infer,
-// src/main.cpp:34-190: same flags; the HTTP server is not built).
+// msst_infer — separate a WAV file with a BSRoformer or MelBandRoformer .csm
+// checkpoint on one MI355X (the file-inference surface of the reference's
+// cudasep_infer, src/main.cpp:34-190: same flags and defaults, fp32 weights
+// unless --fp16; the HTTP server is not built).
 //
 //   msst_infer --model m.csm --input mix.wav [--output dir|file.wav]
 //              [--stem i|-1] [--overlap f] [--fp16|--fp32]
@@ -21,7 +22,7 @@ struct Args {
     std::string model, input, output = "output";
     int stem = 0, device = 0, chunk_batch = 0;
     float overlap = 0.0f;
-    bool fp16 = true, list_stems = false;
+    bool fp16 = false, list_stems = false;
 };
 
 void usage(const char* prog) {
@@ -31,7 +32,7 @@ void usage(const char* prog) {
               << "  --output, -o <path>    output directory or .wav path (default: output)\n"
               << "  --stem, -s <int>       stem to write (default 0, -1 for all)\n"
               << "  --overlap <float>      (0,1) overlap ratio, >= 1 number of overlaps\n"
-              << "  --fp16 / --fp32        fp16 weights with fp32 accumulation (default) / fp32\n"
+              << "  --fp16 / --fp32        fp16 weights with fp32 accumulation / fp32 (default)\n"
               << "  --chunk-batch-size <n> chunks per forward (default 2)\n"
               << "  --device, -d <int>     GPU index (default 0)\n"
               << "  --list-stems           print the model's stems and exit\n";
@@ -77,15 +78,20 @@ int main(int argc, char** argv) {
         HIP_CHECK(hipSetDevice(a.device));
         app::LoadedModel model = app::load_model(a.model, a.fp16);
         if (a.chunk_batch > 0) model.chunk_batch_size = a.chunk_batch;
+        std::cout << "  Model type: " << app::model_type_name(model.type) << "\n"
+                  << "  Sources: " << model.num_sources << ", Sample rate: " << model.sample_rate
+                  << ", Chunk size: " << model.chunk_size << ", Num overlap: " << model.num_overlap
+                  << "\n";
         if (a.list_stems) {
+            std::cout << "\nModel has " << model.num_sources << " source(s).\n";
             for (size_t i = 0; i < model.stem_names.size(); ++i)
                 std::cout << "  [" << i << "] " << model.stem_names[i] << "\n";
             return 0;
         }
         const app::AudioData audio = app::load_wav(a.input);
-        if (audio.channels != model.bsr.audio_channels())
+        if (audio.channels != model.model->audio_channels())
             throw std::runtime_error("the model expects " +
-                                     std::to_string(model.bsr.audio_channels()) + " channels");
+                                     std::to_string(model.model->audio_channels()) + " channels");
         const auto t0 = std::chrono::steady_clock::now();
         Tensor out = app::run_inference(model, audio, a.overlap);
         CudaContext::instance().sync();

@@ -203,24 +203,57 @@ Tensor process_chunked(const Tensor& audio, int chunk_size, int step, int chunk_
     return res;
 }
 
+ModelType detect_model_type(const JsonValue& cfg) {
+    if (cfg.has("model_type")) {
+        const std::string mt = cfg.get_string("model_type", "");
+        if (mt == "mel_band_roformer" || mt == "MelBandRoformer") return ModelType::MelBandRoformer;
+        if (mt == "bs_roformer" || mt == "BSRoformer") return ModelType::BSRoformer;
+        if (mt == "mdx23c" || mt == "MDX23C" || mt == "tfc_tdf") return ModelType::MDX23C;
+        if (mt == "htdemucs" || mt == "HTDemucs") return ModelType::HTDemucs;
+    }
+    if (cfg.has("nfft") && cfg.has("depth") && cfg.has("growth")) return ModelType::HTDemucs;
+    if (cfg.has("num_bands") || cfg.has("mel_scale")) return ModelType::MelBandRoformer;
+    if (cfg.has("freqs_per_bands")) return ModelType::BSRoformer;
+    if (cfg.has("num_scales") || cfg.has("bottleneck_factor") || cfg.has("num_subbands"))
+        return (cfg.has("growth") && cfg.has("depth")) ? ModelType::HTDemucs : ModelType::MDX23C;
+    if (cfg.has("dim") && cfg.has("depth") && cfg.has("dim_head")) return ModelType::BSRoformer;
+    return ModelType::Unknown;
+}
+
+const char* model_type_name(ModelType t) {
+    switch (t) {
+        case ModelType::MelBandRoformer: return "MelBandRoformer";
+        case ModelType::BSRoformer: return "BSRoformer";
+        case ModelType::MDX23C: return "MDX23C";
+        case ModelType::HTDemucs: return "HTDemucs";
+        default: return "Unknown";
+    }
+}
+
 LoadedModel load_model(const std::string& path, bool quantize_fp16) {
     LoadedModel m;
     m.weights = ModelWeights::load(path);
     const JsonValue& cfg = m.weights.config();
-    const std::string mt = cfg.get_string("model_type", "");
-    const bool bsr = mt == "bs_roformer" || mt == "BSRoformer" ||
-                     (mt.empty() && cfg.has("freqs_per_bands") && !cfg.has("num_bands"));
-    if (!bsr)
-        throw std::runtime_error("load_model: only BSRoformer checkpoints are supported here");
+    m.type = detect_model_type(cfg);
+    if (m.type == ModelType::Unknown) throw std::runtime_error("Could not detect model type from config");
+    if (m.type == ModelType::BSRoformer)
+        m.model.reset(new BSRoformer());
+    else if (m.type == ModelType::MelBandRoformer)
+        m.model.reset(new MelBandRoformer());
+    else
+        throw std::runtime_error(std::string("load_model: ") + model_type_name(m.type) +
+                                 " checkpoints are not supported here (BSRoformer and "
+                                 "MelBandRoformer are)");
     g_quantize_fp16 = quantize_fp16;
     if (quantize_fp16) m.weights.convert_linear_weights_to_fp16();
-    m.bsr.load(m.weights);
-    m.num_sources = m.bsr.config().num_stems;
-    m.sample_rate = m.bsr.config().sample_rate;
-    m.chunk_size = cfg.get_int("chunk_size", m.bsr.config().stft_n_fft * 256);
+    m.model->load(m.weights);
+    m.num_sources = m.model->num_stems();
+    m.sample_rate = m.model->sample_rate();
+    m.chunk_size = cfg.get_int("chunk_size", m.model->n_fft() * 256);
+    // inference_app.cpp:42-57: num_overlap from the config, else 2 for the Roformers.
     m.num_overlap = cfg.has("num_overlap") ? std::max(1, cfg.get_int("num_overlap", 1)) : 2;
     m.chunk_batch_size = 2;
-    // inference_app.cpp:343-371: instruments, sources, target_instrument, stem_i.
+    // inference_app.cpp:336-361: instruments, sources, target_instrument, stem_i.
     for (const char* key : {"instruments", "sources"})
         if (m.stem_names.empty() && cfg.has(key) && cfg[key].is_array())
             for (size_t i = 0; i < cfg[key].size(); ++i) m.stem_names.push_back(cfg[key][i].as_string());
@@ -234,7 +267,7 @@ LoadedModel load_model(const std::string& path, bool quantize_fp16) {
 
 Tensor run_inference(LoadedModel& model, const AudioData& audio, float overlap) {
     Tensor x = Tensor::from_cpu_f32(audio.samples.data(), {(int64_t)audio.channels, audio.frames});
-    auto fwd = [&](const Tensor& in) { return model.bsr.forward(in); };
+    auto fwd = [&](const Tensor& in) { return model.model->forward(in); };
     if (model.chunk_size > 0 && audio.frames > model.chunk_size) {
         const int step = resolve_step(model.chunk_size, overlap, model.num_overlap);
         Tensor y = process_chunked(x, model.chunk_size, step, model.chunk_batch_size, fwd);

@@ -1,6 +1,6 @@
 // inference.h — the chunked inference driver and WAV I/O of the reference's
 // cudasep_infer (src/inference_app.{h,cpp}, src/audio_io.{h,cpp}), for the
-// BSRoformer models built here.
+// BSRoformer and MelBandRoformer models built here.
 //
 // process_chunked (inference_app.cpp:100-324, "Generic" mode): the mix is
 // reflect-padded by border = chunk - step, cut into chunks every `step`
@@ -13,10 +13,11 @@
 #pragma once
 
 #include <functional>
+#include <memory>
 #include <string>
 #include <vector>
 
-#include "bs_roformer.h"
+#include "roformer_models.h"
 #include "tensor.h"
 #include "weights.h"
 
@@ -45,9 +46,17 @@ int resolve_step(int chunk_size, float overlap, int default_overlap);
 Tensor process_chunked(const Tensor& audio, int chunk_size, int step, int chunk_batch,
                        const std::function<Tensor(const Tensor&)>& forward);
 
+// inference_app.h (ModelType) and inference_app.cpp:77-98: model_type
+// names first, then the config keys each family carries.  MDX23C and
+// HTDemucs are recognised but not built here (load_model throws).
+enum class ModelType { Unknown, MelBandRoformer, BSRoformer, MDX23C, HTDemucs };
+ModelType detect_model_type(const JsonValue& config);
+const char* model_type_name(ModelType t);
+
 struct LoadedModel {
     ModelWeights weights;
-    BSRoformer bsr;
+    ModelType type = ModelType::Unknown;
+    std::unique_ptr<RoformerModel> model;
     int num_sources = 1;
     int sample_rate = 44100;
     int chunk_size = 0;
@@ -56,8 +65,8 @@ struct LoadedModel {
     std::vector<std::string> stem_names;
 };
 
-// inference_app.cpp:376-447 for BSRoformer checkpoints (other model types
-// throw).  quantize_fp16: the reference's --fp16 load.
+// inference_app.cpp:363-447 for BSRoformer and MelBandRoformer checkpoints
+// (other model types throw).  quantize_fp16: the reference's --fp16 load.
 LoadedModel load_model(const std::string& path, bool quantize_fp16);
 
 // [stems, channels, S] (or [channels, S] for one stem) fp32 on the device.

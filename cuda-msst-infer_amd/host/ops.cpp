@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <stdexcept>
 #include <string>
 
 #include "memory_pool.h"
@@ -147,6 +148,40 @@ Tensor hann_window(int size) {
     Tensor out = Tensor::empty({(int64_t)std::max(size, 0)}, DType::Float32);
     if (size > 0) check(msst_hann_window(out.data_f32(), size, stream()), "hann_window");
     return out;
+}
+
+// ops_misc.cu:469-525
+std::vector<float> mel_filterbank_host(int sr, int n_fft, int n_mels, float fmin, float fmax) {
+    if (sr <= 0 || n_fft < 2 || n_mels < 1)
+        throw std::invalid_argument("mel_filterbank: need sr > 0, n_fft >= 2, n_mels >= 1");
+    if (fmax <= 0.0f) fmax = (float)sr / 2.0f;
+    const int bins = n_fft / 2 + 1;
+    const auto to_mel = [](float hz) { return 2595.0f * std::log10(1.0f + hz / 700.0f); };
+    const auto to_hz = [](float mel) { return 700.0f * (std::pow(10.0f, mel / 2595.0f) - 1.0f); };
+    const float m0 = to_mel(fmin), m1 = to_mel(fmax);
+    std::vector<float> edge((size_t)n_mels + 2);
+    for (int i = 0; i < n_mels + 2; ++i)
+        edge[(size_t)i] = to_hz(m0 + (m1 - m0) * (float)i / (float)(n_mels + 1));
+    std::vector<float> fb((size_t)n_mels * bins, 0.0f);
+    for (int m = 0; m < n_mels; ++m) {
+        const float lo = edge[(size_t)m], mid = edge[(size_t)m + 1], hi = edge[(size_t)m + 2];
+        for (int f = 0; f < bins; ++f) {
+            const float hz = (float)sr * (float)f / (float)n_fft;
+            float v = 0.0f;
+            if (hz >= lo && hz <= mid) {
+                if (mid - lo > 0.0f) v = (hz - lo) / (mid - lo);
+            } else if (hz > mid && hz <= hi) {
+                if (hi - mid > 0.0f) v = (hi - hz) / (hi - mid);
+            }
+            fb[(size_t)m * bins + f] = v;
+        }
+    }
+    return fb;
+}
+
+Tensor mel_filterbank(int sr, int n_fft, int n_mels, float fmin, float fmax) {
+    const std::vector<float> fb = mel_filterbank_host(sr, n_fft, n_mels, fmin, fmax);
+    return Tensor::from_cpu_f32(fb.data(), {(int64_t)n_mels, (int64_t)(n_fft / 2 + 1)});
 }
 
 // ops_elementwise.cu:84-88, :138

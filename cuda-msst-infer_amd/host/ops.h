@@ -82,6 +82,16 @@ Tensor istft(const Tensor& complex_spec, int n_fft, int hop_length, int win_leng
              bool normalized = false);
 Tensor hann_window(int size);
 
+// ops.h:124 (ops_misc.cu:469-525): triangular HTK-mel filterbank
+// [n_mels, n_fft/2 + 1] (mel = 2595 log10(1 + f/700); n_mels + 2 points
+// evenly spaced in mel between fmin and fmax, fmax <= 0 meaning sr / 2;
+// bin f at sr * f / n_fft), computed in float on the host like the
+// reference's.  mel_filterbank_host returns the row-major values,
+// mel_filterbank the same uploaded to the device.
+std::vector<float> mel_filterbank_host(int sr, int n_fft, int n_mels, float fmin = 0.0f,
+                                       float fmax = 0.0f);
+Tensor mel_filterbank(int sr, int n_fft, int n_mels, float fmin = 0.0f, float fmax = 0.0f);
+
 // ops_elementwise.cu:84-88, :138 (tanhf) and :321-388 (first * sigmoid(second));
 // glu splits the last dimension only (the Roformers' use, dim = -1).
 Tensor tanh_act(const Tensor& x);

@@ -559,3 +559,32 @@ void orc_hann_window(float* out, int size) {
         out[i] = size == 1 ? 1.0f
                            : (float)(0.5 * (1.0 - cos(2.0 * 3.14159265358979323846 * i / size)));
 }
+
+/* ops_misc.cu:469-525: mel = 2595 log10(1 + hz / 700); n_mels + 2 edges
+ * evenly spaced in mel; bin f sits at sr * f / n_fft; rising edge on
+ * [left, centre], falling edge on (centre, right]; all in float. */
+void orc_mel_filterbank(float* out, int sr, int n_fft, int n_mels, float fmin, float fmax) {
+    const int bins = n_fft / 2 + 1;
+    if (fmax <= 0.0f) fmax = (float)sr / 2.0f;
+    const float mlo = 2595.0f * log10f(1.0f + fmin / 700.0f);
+    const float mhi = 2595.0f * log10f(1.0f + fmax / 700.0f);
+    float* hz = (float*)malloc(sizeof(float) * (size_t)(n_mels + 2));
+    for (int i = 0; i < n_mels + 2; ++i) {
+        const float mel = mlo + (mhi - mlo) * (float)i / (float)(n_mels + 1);
+        hz[i] = 700.0f * (powf(10.0f, mel / 2595.0f) - 1.0f);
+    }
+    for (int m = 0; m < n_mels; ++m) {
+        const float l = hz[m], c = hz[m + 1], r = hz[m + 2];
+        for (int f = 0; f < bins; ++f) {
+            const float x = (float)sr * (float)f / (float)n_fft;
+            float v = 0.0f;
+            if (x >= l && x <= c) {
+                if (c - l > 0.0f) v = (x - l) / (c - l);
+            } else if (x > c && x <= r) {
+                if (r - c > 0.0f) v = (r - x) / (r - c);
+            }
+            out[(size_t)m * bins + f] = v;
+        }
+    }
+    free(hz);
+}

@@ -160,6 +160,10 @@ void orc_istft(const float* spec, int64_t B, int64_t T, int n_fft, int hop,
 /* Periodic Hann window (ops_stft.cu:254-262). */
 void orc_hann_window(float* out, int size);
 
+/* Triangular HTK-mel filterbank out[n_mels, n_fft/2 + 1] in float, step for
+ * step as ops_misc.cu:469-525 (fmax <= 0 -> sr / 2). */
+void orc_mel_filterbank(float* out, int sr, int n_fft, int n_mels, float fmin, float fmax);
+
 #ifdef __cplusplus
 }
 #endif

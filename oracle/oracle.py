@@ -76,6 +76,8 @@ def _declare(l: ctypes.CDLL) -> None:
     l.orc_istft.argtypes = [_fp, _i64, _i64, ctypes.c_int, ctypes.c_int, _fp, _i64, ctypes.c_int,
                             ctypes.c_int, _fp]
     l.orc_hann_window.argtypes = [_fp, ctypes.c_int]
+    l.orc_mel_filterbank.argtypes = [_fp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_float, ctypes.c_float]
     l.orc_mask_merge.argtypes = [_fp, _i64, _fp, _i64, _i64, _i64, _i64, _ip, _i64, ctypes.c_int,
                                  _fp]
 
@@ -328,21 +330,40 @@ def istft(spec, n_fft, hop, window, length=-1, center=True, normalized=False) ->
 
 
 # ------------------------------------------------------------------ BSRoformer
-def bsroformer_forward(cfg: dict, w: dict, audio) -> np.ndarray:
-    """BSRoformer::forward (model_bs_roformer.cu:420-609) composed from the
-    functions above.  cfg: the checkpoint config; w: name -> fp32 array (the
-    reference's weight names); audio [B, ch, S] -> [B, stems, ch, S']."""
+def mel_filterbank(sr: int, n_fft: int, n_mels: int, fmin: float = 0.0,
+                   fmax: float = 0.0) -> np.ndarray:
+    """ops::mel_filterbank (ops_misc.cu:469-525): [n_mels, n_fft/2 + 1] fp32."""
+    out = np.empty((n_mels, n_fft // 2 + 1), np.float32)
+    lib().orc_mel_filterbank(_p(out), sr, n_fft, n_mels, ctypes.c_float(fmin),
+                             ctypes.c_float(fmax))
+    return out
+
+
+def mel_bands(sr: int, n_fft: int, num_bands: int, channels: int):
+    """MelBandRoformer::compute_mel_bands (model_mel_band_roformer.cu:214-308):
+    the filterbank with its two corners forced to 1, thresholded at > 0.
+    Returns (freq_indices with the channels interleaved as f * ch + s,
+    bins per band)."""
+    fb = mel_filterbank(sr, n_fft, num_bands)
+    fb[0, 0] = 1.0
+    fb[-1, -1] = 1.0
+    on = fb > 0
+    counts = on.sum(axis=1).astype(np.int64)
+    mono = np.concatenate([np.nonzero(on[b])[0] for b in range(num_bands)]).astype(np.int64)
+    fidx = (mono[:, None] * channels + np.arange(channels)[None, :]).reshape(-1)
+    return fidx, counts
+
+
+def _roformer_forward(cfg: dict, w: dict, audio, dims, fidx, depth: int, L: int,
+                      per_norm: bool, final_gamma) -> np.ndarray:
     audio = _f32(audio)
     B, ch, S = audio.shape
     n_fft, hop = cfg.get("stft_n_fft", 2048), cfg.get("stft_hop_length", 441)
     norm = bool(cfg.get("stft_normalized", False))
-    stems, depth = cfg.get("num_stems", 1), cfg.get("depth", 12)
-    L = cfg.get("mask_estimator_depth", 1)
-    fpb = cfg["freqs_per_bands"]
-    dims = [2 * f * ch for f in fpb]
+    stems = cfg.get("num_stems", 1)
     win = hann_window(n_fft)
     spec = stft(audio.reshape(B * ch, S), n_fft, hop, win, True, norm)      # [B*ch, F, T, 2]
-    x = band_gather(spec, B)
+    x = band_gather(spec, B, fidx)
     nb = len(dims)
     feats = band_split(
         x.reshape(-1, x.shape[-1]), dims,
@@ -359,9 +380,9 @@ def bsroformer_forward(cfg: dict, w: dict, audio) -> np.ndarray:
                 w[p + ".0.norm.gamma"], w[p + ".0.to_qkv.weight"], w[p + ".0.to_gates.weight"],
                 w[p + ".0.to_gates.bias"], w[p + ".0.to_out.0.weight"], w[p + ".1.net.0.gamma"],
                 w[p + ".1.net.1.weight"], w[p + ".1.net.1.bias"], w[p + ".1.net.4.weight"],
-                w[p + ".1.net.4.bias"]))
+                w[p + ".1.net.4.bias"], w[f"layers.{d}.{t}.norm.gamma"] if per_norm else None))
     feats = roformer_stack(feats, layers, cfg.get("heads", 8), cfg.get("dim_head", 64),
-                           w["final_norm.gamma"])
+                           final_gamma)
     masks = []
     for s in range(stems):
         ws = [[w[f"mask_estimators.{s}.to_freqs.{b}.0.{2 * i}.weight"] for i in range(L)]
@@ -369,10 +390,38 @@ def bsroformer_forward(cfg: dict, w: dict, audio) -> np.ndarray:
         bs = [[w[f"mask_estimators.{s}.to_freqs.{b}.0.{2 * i}.bias"] for i in range(L)]
               for b in range(nb)]
         masks.append(mask_estimator(feats.reshape(B * T, nb, -1), dims, ws, bs).reshape(B, T, -1))
-    merged = mask_merge(np.stack(masks), spec, B, None, bool(cfg.get("zero_dc", True)))
+    merged = mask_merge(np.stack(masks), spec, B, fidx, bool(cfg.get("zero_dc", True)))
     length = S if cfg.get("match_input_audio_length", False) else -1
     y = istft(merged, n_fft, hop, win, length, True, norm)
     return y.reshape(B, stems, ch, -1)
+
+
+def bsroformer_forward(cfg: dict, w: dict, audio) -> np.ndarray:
+    """BSRoformer::forward (model_bs_roformer.cu:420-609) composed from the
+    functions above.  cfg: the checkpoint config; w: name -> fp32 array (the
+    reference's weight names); audio [B, ch, S] -> [B, stems, ch, S']."""
+    ch = np.shape(audio)[1]
+    dims = [2 * f * ch for f in cfg["freqs_per_bands"]]
+    return _roformer_forward(cfg, w, audio, dims, None, cfg.get("depth", 12),
+                             cfg.get("mask_estimator_depth", 1), False, w["final_norm.gamma"])
+
+
+def melbandroformer_forward(cfg: dict, w: dict, audio) -> np.ndarray:
+    """MelBandRoformer::forward (model_mel_band_roformer.cu:745-1040): bands
+    from w["__precomputed__.freq_indices"] / ["__precomputed__.num_freqs_per_band"]
+    when present (model_mel_band_roformer.cu:322-375), else mel_bands; a norm
+    closing every transformer (layers.{d}.{t}.norm.gamma), no final norm, and
+    mask_estimator_depth + 1 linears per band MLP."""
+    ch = np.shape(audio)[1]
+    if "__precomputed__.freq_indices" in w:
+        fidx = np.asarray(w["__precomputed__.freq_indices"], np.int64)
+        counts = np.asarray(w["__precomputed__.num_freqs_per_band"], np.int64)
+    else:
+        fidx, counts = mel_bands(cfg.get("sample_rate", 44100), cfg.get("stft_n_fft", 2048),
+                                 cfg.get("num_bands", 60), ch)
+    dims = [int(2 * c * ch) for c in counts]
+    return _roformer_forward(cfg, w, audio, dims, fidx, cfg.get("depth", 6),
+                             cfg.get("mask_estimator_depth", 2) + 1, True, None)
 
 
 def process_chunked(audio, chunk_size: int, step: int, batch: int, forward) -> np.ndarray:

@@ -1,12 +1,15 @@
 """End to end through the msst_infer CLI (the reference's cudasep_infer file
-path): a synthetic BSRoformer .csm (random weights under the reference's
-names), a stereo WAV in, float WAVs out, compared with the oracle's
-BSRoformer forward run through the oracle's chunked driver.
+path): synthetic BSRoformer and MelBandRoformer .csm files (random weights
+under the reference's names), a stereo WAV in, float WAVs out, compared with
+the oracle's model forward run through the oracle's chunked driver.
 
-Config: dim 128, depth 1, 2 heads, 2 stems, 19 bands over a 256-point STFT
-(hop 64), mask-estimator MLP of 2 linears, chunk 4096 with 2 overlaps, so a
-10000-sample track takes the chunked path (border reflect padding, batch 2,
-a zero-padded last chunk) and a 3000-sample one the direct path.
+BSRoformer: dim 128, depth 1, 2 heads, 2 stems, 19 bands over a 256-point
+STFT (hop 64), mask-estimator MLP of 2 linears.  MelBandRoformer: the same
+trunk with 16 overlapping HTK-mel bands computed at load (or 16 precomputed
+overlapping bands stored in the file), per-transformer norms, mask MLP of 3
+linears.  Chunk 4096 with 2 overlaps, so a 10000-sample track takes the
+chunked path (border reflect padding, batch 2, a zero-padded last chunk)
+and a 3000-sample one the direct path.
 Tolerances: fp32 (--fp32) 1e-4, fp16 weights (--fp16) 2e-2, normwise per stem.
 """
 from __future__ import annotations
@@ -31,6 +34,23 @@ CFG = {"model_type": "bs_roformer", "dim": 128, "depth": 1, "heads": 2, "dim_hea
        "zero_dc": True, "stft_n_fft": 256, "stft_hop_length": 64, "stft_win_length": 256,
        "freqs_per_bands": [4] * 8 + [8] * 8 + [16] * 2 + [1], "chunk_size": 4096,
        "num_overlap": 2, "sample_rate": 44100, "instruments": ["vocals", "other"]}
+
+
+MBR_CFG = {"model_type": "mel_band_roformer", "dim": 128, "depth": 1, "heads": 2,
+           "dim_head": 64, "stereo": True, "num_stems": 2, "num_bands": 16,
+           "mask_estimator_depth": 2, "mlp_expansion_factor": 4, "zero_dc": True,
+           "stft_n_fft": 256, "stft_hop_length": 64, "stft_win_length": 256,
+           "chunk_size": 4096, "num_overlap": 2, "sample_rate": 44100,
+           "instruments": ["vocals", "other"]}
+
+
+def mbr_model(oracle, cfg, seed, unit_mask=False, precomputed=False):
+    F = cfg["stft_n_fft"] // 2 + 1
+    if precomputed:
+        bands = csm_file.overlapping_bands(F, 2, cfg["num_bands"])
+        return csm_file.mbr_checkpoint(cfg, bands[1], seed, unit_mask, precomputed=bands)
+    _, counts = oracle.mel_bands(cfg["sample_rate"], cfg["stft_n_fft"], cfg["num_bands"], 2)
+    return csm_file.mbr_checkpoint(cfg, counts, seed, unit_mask)
 
 
 def run_cli(args):
@@ -60,7 +80,8 @@ def separate(tmp_path, cfg, w, audio, mode):
 def oracle_separate(oracle, cfg, w, audio):
     chunk = cfg["chunk_size"]
     step = chunk // cfg["num_overlap"]
-    fwd = lambda b: oracle.bsroformer_forward(cfg, w, b)
+    model = oracle.melbandroformer_forward if "num_bands" in cfg else oracle.bsroformer_forward
+    fwd = lambda b: model(cfg, w, b)
     if audio.shape[1] > chunk:
         y = oracle.process_chunked(audio, chunk, step, 2, fwd)
         return y.reshape(cfg["num_stems"], audio.shape[0], -1)
@@ -74,13 +95,55 @@ def test_cli_matches_oracle(tmp_path, oracle, cuda, S, mode):
     audio = (0.3 * rng.standard_normal((2, S))).astype(np.float32)
     w = csm_file.bsr_checkpoint(CFG, seed=2)
     y = separate(tmp_path, CFG, w, audio, mode)
-    wr = {k: (v.astype(np.float16).astype(np.float32) if (mode == "fp16" and v.ndim == 2) else v)
-          for k, v in w.items()}
-    r = oracle_separate(oracle, CFG, wr, audio)
+    r = oracle_separate(oracle, CFG, _fp16_view(w, mode), audio)
     assert y.shape == r.shape
     tol = 1e-4 if mode == "fp32" else TOL_F16
     for s in range(y.shape[0]):
         assert rel_err(y[s], r[s]) < tol, (s, rel_err(y[s], r[s]))
+
+
+def _fp16_view(w, mode):
+    return {k: (v.astype(np.float16).astype(np.float32) if (mode == "fp16" and v.ndim == 2) else v)
+            for k, v in w.items()}
+
+
+@pytest.mark.parametrize("S", [10000, 3000])
+@pytest.mark.parametrize("mode", ["fp32", "fp16"])
+@pytest.mark.parametrize("bands", ["mel", "precomputed"])
+def test_cli_melband_matches_oracle(tmp_path, oracle, cuda, S, mode, bands):
+    rng = np.random.default_rng(S + 1)
+    audio = (0.3 * rng.standard_normal((2, S))).astype(np.float32)
+    w = mbr_model(oracle, MBR_CFG, seed=5, precomputed=bands == "precomputed")
+    y = separate(tmp_path, MBR_CFG, w, audio, mode)
+    r = oracle_separate(oracle, MBR_CFG, _fp16_view(w, mode), audio)
+    assert y.shape == r.shape
+    tol = 1e-4 if mode == "fp32" else TOL_F16
+    for s in range(y.shape[0]):
+        assert rel_err(y[s], r[s]) < tol, (s, rel_err(y[s], r[s]))
+
+
+def test_cli_melband_detected_without_model_type(tmp_path, oracle, cuda):
+    """No model_type: num_bands selects MelBandRoformer
+    (inference_app.cpp:87)."""
+    cfg = {k: v for k, v in MBR_CFG.items() if k != "model_type"}
+    w = mbr_model(oracle, cfg, seed=6)
+    model = tmp_path / "m.csm"
+    csm_file.write_csm(model, cfg, w)
+    out = run_cli(["--model", str(model), "--list-stems"])
+    assert "Model type: MelBandRoformer" in out and "Model has 2 source(s)" in out
+
+
+@pytest.mark.parametrize("bands", ["mel", "precomputed"])
+def test_cli_melband_unit_mask_returns_the_mix(tmp_path, oracle, cuda, bands):
+    """Masks of 1 + 0i on every band: the scatter-mean over overlapping
+    bands is 1 on every bin, so every stem is the mix."""
+    cfg = copy.deepcopy(MBR_CFG)
+    cfg["zero_dc"] = False
+    w = mbr_model(oracle, cfg, seed=7, unit_mask=True, precomputed=bands == "precomputed")
+    audio = (0.5 * np.random.default_rng(10).standard_normal((2, 10000))).astype(np.float32)
+    y = separate(tmp_path, cfg, w, audio, "fp16")
+    for s in range(y.shape[0]):
+        assert rel_err(y[s], audio) < 1e-5
 
 
 def test_cli_unit_mask_returns_the_mix(tmp_path, cuda):
@@ -100,7 +163,7 @@ def test_cli_list_stems_and_errors(tmp_path, cuda):
     model = tmp_path / "m.csm"
     csm_file.write_csm(model, CFG, csm_file.bsr_checkpoint(CFG, seed=4))
     out = run_cli(["--model", str(model), "--list-stems"])
-    assert "[0] vocals" in out and "[1] other" in out
+    assert "[0] vocals" in out and "[1] other" in out and "Model type: BSRoformer" in out
     r = subprocess.run([CLI, "--model", str(tmp_path / "missing.csm"), "--input", "x.wav"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 1 and "cannot open" in r.stderr
@@ -109,3 +172,8 @@ def test_cli_list_stems_and_errors(tmp_path, cuda):
     r = subprocess.run([CLI, "--model", str(bad), "--list-stems"], capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 1 and "magic" in r.stderr
+    mdx = tmp_path / "mdx.csm"
+    csm_file.write_csm(mdx, {"model_type": "mdx23c", "num_subbands": 4}, {})
+    r = subprocess.run([CLI, "--model", str(mdx), "--list-stems"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 1 and "MDX23C checkpoints are not supported" in r.stderr

@@ -540,3 +540,101 @@ def test_bsroformer_forward_unit_mask_returns_input(oracle):
     assert y.shape == (1, 2, 2, 64 * 40)
     for s in range(2):
         assert rel_err(y[0, s], x[0]) < 1e-5
+
+
+def _htk_triangles_f64(sr, n_fft, n_mels, fmin=0.0, fmax=0.0):
+    """Textbook HTK-mel triangles in float64, written as the clipped minimum
+    of the two slopes (a different formulation from the piecewise one)."""
+    fmax = fmax if fmax > 0 else sr / 2
+    hz2mel = lambda f: 2595.0 * np.log10(1.0 + f / 700.0)
+    mel2hz = lambda m: 700.0 * (10.0 ** (m / 2595.0) - 1.0)
+    e = mel2hz(np.linspace(hz2mel(fmin), hz2mel(fmax), n_mels + 2))
+    f = sr * np.arange(n_fft // 2 + 1) / n_fft
+    up = (f[None, :] - e[:-2, None]) / (e[1:-1, None] - e[:-2, None])
+    down = (e[2:, None] - f[None, :]) / (e[2:, None] - e[1:-1, None])
+    return np.maximum(0.0, np.minimum(up, down)), e, f
+
+
+MEL_CASES = [(44100, 2048, 60, 0.0, 0.0), (44100, 256, 16, 0.0, 0.0),
+             (48000, 1024, 40, 0.0, 0.0), (16000, 512, 10, 50.0, 7000.0)]
+
+
+@pytest.mark.parametrize("sr,n_fft,n_mels,fmin,fmax", MEL_CASES)
+def test_mel_filterbank_matches_float64_triangles(oracle, sr, n_fft, n_mels, fmin, fmax):
+    fb = oracle.mel_filterbank(sr, n_fft, n_mels, fmin, fmax)
+    ref, e, f = _htk_triangles_f64(sr, n_fft, n_mels, fmin, fmax)
+    assert fb.shape == ref.shape
+    np.testing.assert_allclose(fb, ref, atol=2e-4)
+    # Membership agrees wherever the bin is not within 0.05 Hz of an edge
+    # (where float and float64 may round to opposite sides).
+    tie = (np.abs(f[None, :] - e[:-2, None]) < 0.05) | (np.abs(f[None, :] - e[2:, None]) < 0.05)
+    assert np.array_equal((fb > 0)[~tie], (ref > 0)[~tie])
+
+
+@pytest.mark.parametrize("sr,n_fft,n_mels,fmin,fmax", MEL_CASES)
+def test_mel_filterbank_partition_of_unity(oracle, sr, n_fft, n_mels, fmin, fmax):
+    """Adjacent HTK triangles share their edges, so between the first and
+    the last centre the filters sum to 1 on every bin (an index slip in the
+    edges breaks this)."""
+    fb = oracle.mel_filterbank(sr, n_fft, n_mels, fmin, fmax)
+    _, e, f = _htk_triangles_f64(sr, n_fft, n_mels, fmin, fmax)
+    inner = (f >= e[1] + 1e-3) & (f <= e[n_mels] - 1e-3)
+    assert inner.sum() > 0
+    np.testing.assert_allclose(fb.sum(axis=0)[inner], 1.0, atol=2e-5)
+    assert fb.min() >= 0.0 and fb.max() <= 1.0 + 1e-6
+
+
+def test_mel_filterbank_single_band_closed_form(oracle):
+    """n_mels 1: one triangle from fmin to fmax peaking at the mel midpoint."""
+    sr, n_fft = 22050, 64
+    fb = oracle.mel_filterbank(sr, n_fft, 1)[0]
+    mid = 700.0 * (10.0 ** ((2595.0 * np.log10(1.0 + sr / 2 / 700.0)) / 2 / 2595.0) - 1.0)
+    f = sr * np.arange(n_fft // 2 + 1) / n_fft
+    ref = np.where(f <= mid, f / mid, (sr / 2 - f) / (sr / 2 - mid))
+    np.testing.assert_allclose(fb, ref, atol=1e-5)
+
+
+@pytest.mark.parametrize("sr,n_fft,nb,ch", [(44100, 2048, 60, 2), (44100, 256, 16, 2),
+                                            (44100, 2048, 60, 1)])
+def test_mel_bands_cover_every_bin_and_interleave(oracle, sr, n_fft, nb, ch):
+    fidx, counts = oracle.mel_bands(sr, n_fft, nb, ch)
+    F = n_fft // 2 + 1
+    assert len(counts) == nb and counts.min() >= 1 and len(fidx) == counts.sum() * ch
+    mono = fidx[::ch] // ch
+    for s in range(ch):
+        assert np.array_equal(fidx[s::ch], mono * ch + s)
+    assert np.array_equal(np.unique(mono), np.arange(F))   # every bin in some band
+    off = np.concatenate([[0], np.cumsum(counts)])
+    first = mono[off[:-1]]
+    last = mono[off[1:] - 1]
+    assert first[0] == 0 and last[-1] == F - 1               # the two forced corners
+    assert np.all(np.diff(first) >= 0) and np.all(np.diff(last) >= 0)
+    for b in range(nb):                                      # contiguous runs of bins
+        seg = mono[off[b]:off[b + 1]]
+        assert np.array_equal(seg, np.arange(seg[0], seg[0] + len(seg)))
+
+
+SMALL_MBR = {"model_type": "mel_band_roformer", "dim": 64, "depth": 1, "heads": 2,
+             "dim_head": 32, "stereo": True, "num_stems": 2, "num_bands": 16,
+             "mask_estimator_depth": 2, "mlp_expansion_factor": 4, "zero_dc": False,
+             "stft_n_fft": 256, "stft_hop_length": 64, "stft_win_length": 256,
+             "sample_rate": 44100}
+
+
+@pytest.mark.parametrize("precomputed", [False, True])
+def test_melbandroformer_forward_unit_mask_returns_input(oracle, precomputed):
+    """Unit masks on overlapping bands: the scatter-mean is 1 on every bin,
+    so the forward is istft(stft(x)) = x."""
+    import csm_file
+    if precomputed:
+        fidx, counts = csm_file.overlapping_bands(129, 2, 16)
+        w = csm_file.mbr_checkpoint(SMALL_MBR, counts, seed=2, unit_mask=True,
+                                    precomputed=(fidx, counts))
+    else:
+        _, counts = oracle.mel_bands(44100, 256, 16, 2)
+        w = csm_file.mbr_checkpoint(SMALL_MBR, counts, seed=2, unit_mask=True)
+    x = rnd(1, 2, 64 * 40)
+    y = oracle.melbandroformer_forward(SMALL_MBR, w, x)
+    assert y.shape == (1, 2, 2, 64 * 40)
+    for s in range(2):
+        assert rel_err(y[0, s], x[0]) < 1e-5
