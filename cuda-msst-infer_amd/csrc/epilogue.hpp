@@ -35,6 +35,16 @@ constexpr int pick_ip() {
     return ip;
 }
 
+// A wave-uniform pointer held in SGPRs (buffer resources built from it need
+// no per-lane loop).
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
 // Epilogue variants of store_tile_lds.
 constexpr int kEpiPlain = 0;  // act(acc + bias)
 constexpr int kEpiRes = 1;    // act(acc + bias) + residual
@@ -71,6 +81,10 @@ struct EpiRope {
 // rows, or RoPE cos/sin rows) are issued before the stores of batch b: loads
 // and stores share one in-order vmcnt on CDNA, so a load issued after a
 // batch of stores could only be waited for together with those stores.
+// Whole-width wave tiles (the common case) store through buffer resources
+// bounded to the rows below M, so the read-back loop has no per-row branch:
+// with branches, the compiler's conservative wait at each join made every
+// store wait for all earlier ones (a full memory round trip per store).
 // EPI and ACT are compile-time (ACT < 0: the runtime `act` argument).
 // Caller: the wave's region is free (after a barrier that follows the last
 // read of the k-loop's tiles).
@@ -106,9 +120,135 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
 #pragma unroll
         for (int e = 0; e < 4; ++e) bv[e] = (col + e < N) ? bias[col + e] : 0.0f;
     }
-    auto batch_row = [&](int b, int u) {  // global row of batch b, slot u
-        return row0 + (b / BPP) * IP * 32 + ((b % BPP) * U + u) * RPI + rr;
+    auto local_row = [&](int b, int u) {  // row of batch b, slot u within the wave tile
+        return (b / BPP) * IP * 32 + ((b % BPP) * U + u) * RPI + rr;
     };
+    auto batch_row = [&](int b, int u) { return row0 + local_row(b, u); };
+    // Stage pass p (fragment rows p*IP .. p*IP+IP-1) into the region.
+    auto stage = [&](int p) {
+#pragma unroll
+        for (int ii = 0; ii < IP; ++ii)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                if constexpr (TR) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const f16x& a = acc[p * IP + ii][j];
+                        *reinterpret_cast<f4*>(wlds + (ii * 32 + lrow) * LDW + j * 32 + 8 * g +
+                                               4 * lh) = f4{a[4 * g], a[4 * g + 1], a[4 * g + 2],
+                                                            a[4 * g + 3]};
+                    }
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int r = ii * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                        wlds[r * LDW + j * 32 + lrow] = acc[p * IP + ii][j][v];
+                    }
+                }
+            }
+    };
+    auto finish = [&](f4 v, const f4& rv) {  // bias, activation, residual / RoPE
+        f4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if constexpr (ACT >= 0)
+                o[e] = act_fixed<ACT>(v[e] + bv[e]);
+            else
+                o[e] = act_apply(v[e] + bv[e], act);
+        }
+        if constexpr (EPI == kEpiRes) o += rv;
+        if constexpr (EPI == kEpiRope) {
+            if (rope_on) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float a = (float)(half_t)o[2 * e];
+                    const float bb = (float)(half_t)o[2 * e + 1];
+                    o[2 * e] = a * rv[e] - bb * rv[2 + e];
+                    o[2 * e + 1] = a * rv[2 + e] + bb * rv[e];
+                }
+            }
+        }
+        return o;
+    };
+    auto rope_batch = [&](int b, f4 (&rv)[U]) {  // (cos, cos, sin, sin) of the lane's 2 pairs
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int grow = min(batch_row(b, u), M - 1);
+            int rem, pos;
+            const int q = divmod24(grow, rope.div, rope.inv_div, rem);
+            divmod24(q, rope.mod, rope.inv_mod, pos);
+            const int t = pos * (rope.dh >> 1) + pair;
+            const float2 c = *reinterpret_cast<const float2*>(rope.cos + t);
+            const float2 sn = *reinterpret_cast<const float2*>(rope.sin + t);
+            rv[u] = f4{c.x, c.y, sn.x, sn.y};
+        }
+    };
+
+    if (full) {
+        // Whole-width wave tile: buffer accesses bounded to the wave's rows
+        // below M, so rows past M read zero and their stores are dropped by
+        // the hardware.  The loop is then straight-line code, and each wait
+        // the compiler places covers exactly the data it needs: no per-row
+        // branch forces a wait for every earlier store.
+        // row0 is wave-uniform; readfirstlane keeps the resources in SGPRs.
+        const int wrow0 = __builtin_amdgcn_readfirstlane(row0);
+        const int nrows = max(0, min(M - wrow0, MI * 32));
+        const int64_t rbase = (int64_t)max(wrow0, 0) * N;
+        const int nbytes = __builtin_amdgcn_readfirstlane(nrows * N * (int)sizeof(OutT));
+        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+            uniform_ptr(out + rbase), (short)0, nbytes, 0x00020000);
+        __amdgpu_buffer_rsrc_t rr_src = ro;
+        if constexpr (EPI == kEpiRes)
+            rr_src = __builtin_amdgcn_make_buffer_rsrc(
+                uniform_ptr(const_cast<OutT*>(residual) + rbase), (short)0, nbytes, 0x00020000);
+        auto off = [&](int b, int u) { return (local_row(b, u) * N + col) * (int)sizeof(OutT); };
+        auto load_res = [&](int b, f4 (&rv)[U]) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if constexpr (std::is_same<OutT, float>::value) {
+                    rv[u] = __builtin_bit_cast(
+                        f4, __builtin_amdgcn_raw_buffer_load_b128(rr_src, off(b, u), 0, 0));
+                } else {
+                    const h4 h = __builtin_bit_cast(
+                        h4, __builtin_amdgcn_raw_buffer_load_b64(rr_src, off(b, u), 0, 0));
+                    rv[u] = f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+                }
+            }
+        };
+        f4 rb[2][U];
+        if constexpr (EPI == kEpiRes) load_res(0, rb[0]);
+        if constexpr (EPI == kEpiRope) {
+            if (rope_on) rope_batch(0, rb[0]);
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (b % BPP == 0) stage(b / BPP);
+            if (b + 1 < NB) {
+                if constexpr (EPI == kEpiRes) load_res(b + 1, rb[(b + 1) & 1]);
+                if constexpr (EPI == kEpiRope) {
+                    if (rope_on) rope_batch(b + 1, rb[(b + 1) & 1]);
+                }
+            }
+            const int it0 = (b % BPP) * U;
+            f4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                v[u] = *reinterpret_cast<const f4*>(wlds + ((it0 + u) * RPI + rr) * LDW + cq * 4);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const f4 o = finish(v[u], rb[b & 1][u]);
+                if constexpr (std::is_same<OutT, float>::value) {
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, o), ro, off(b, u),
+                                                           0, 0);
+                } else {
+                    const h4 h = h4{(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
+                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, h), ro, off(b, u),
+                                                          0, 0);
+                }
+            }
+        }
+        return;
+    }
     // rv: residual values, or (cos, cos, sin, sin) of the lane's 2 pairs.
     auto load_batch = [&](int b, f4 (&rv)[U]) {
         if constexpr (EPI == kEpiRes) {
@@ -128,19 +268,7 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
                 }
             }
         } else if constexpr (EPI == kEpiRope) {
-            if (rope_on) {
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int grow = min(batch_row(b, u), M - 1);
-                    int rem, pos;
-                    const int q = divmod24(grow, rope.div, rope.inv_div, rem);
-                    divmod24(q, rope.mod, rope.inv_mod, pos);
-                    const int t = pos * (rope.dh >> 1) + pair;
-                    const float2 c = *reinterpret_cast<const float2*>(rope.cos + t);
-                    const float2 sn = *reinterpret_cast<const float2*>(rope.sin + t);
-                    rv[u] = f4{c.x, c.y, sn.x, sn.y};
-                }
-            }
+            if (rope_on) rope_batch(b, rv);
         }
     };
     f4 rbuf[2][U];
@@ -148,29 +276,7 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int p = b / BPP;
-        if (b % BPP == 0) {
-            // Stage pass p (fragment rows p*IP .. p*IP+IP-1) into the region.
-#pragma unroll
-            for (int ii = 0; ii < IP; ++ii)
-#pragma unroll
-                for (int j = 0; j < NI; ++j) {
-                    if constexpr (TR) {
-#pragma unroll
-                        for (int g = 0; g < 4; ++g) {
-                            const f16x& a = acc[p * IP + ii][j];
-                            *reinterpret_cast<f4*>(wlds + (ii * 32 + lrow) * LDW + j * 32 +
-                                                   8 * g + 4 * lh) =
-                                f4{a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
-                        }
-                    } else {
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const int r = ii * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                            wlds[r * LDW + j * 32 + lrow] = acc[p * IP + ii][j][v];
-                        }
-                    }
-                }
-        }
+        if (b % BPP == 0) stage(p);
         if constexpr (LOADS) {
             if (b + 1 < NB) load_batch(b + 1, rbuf[(b + 1) & 1]);
         }
@@ -183,27 +289,7 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
         for (int u = 0; u < U; ++u) {
             const int grow = batch_row(b, u);
             if (grow < M) {
-                f4 o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if constexpr (ACT >= 0)
-                        o[e] = act_fixed<ACT>(v[u][e] + bv[e]);
-                    else
-                        o[e] = act_apply(v[u][e] + bv[e], act);
-                }
-                if constexpr (EPI == kEpiRes) o += rbuf[b & 1][u];
-                if constexpr (EPI == kEpiRope) {
-                    if (rope_on) {
-                        const f4 cs = rbuf[b & 1][u];
-#pragma unroll
-                        for (int e = 0; e < 2; ++e) {
-                            const float a = (float)(half_t)o[2 * e];
-                            const float bb = (float)(half_t)o[2 * e + 1];
-                            o[2 * e] = a * cs[e] - bb * cs[2 + e];
-                            o[2 * e + 1] = a * cs[2 + e] + bb * cs[e];
-                        }
-                    }
-                }
+                const f4 o = finish(v[u], rbuf[b & 1][u]);
                 const int64_t idx = (int64_t)grow * N + col;
                 if (full) {
                     st4<OutT>(out + idx, o);

@@ -335,11 +335,12 @@ __device__ __forceinline__ int chunk_swz(int r) {
 }
 
 // BK = 64 (128-byte LDS rows) or 32 (64-byte rows).  NSTG = LDS ring
-// stages: the DMA of k-tile t + NSTG - 1 is issued while tile t computes,
-// so a load has NSTG - 1 k-tiles of MFMA time to land.  The per-k-tile
-// barrier is fence-free (lds_barrier): __syncthreads() would add
-// s_waitcnt vmcnt(0) and wait for the younger stages too, serialising the
-// ring.  MINB = workgroups per CU the register/LDS budget is sized for
+// stages: the prologue fills the whole ring, and the DMA of k-tile t + NSTG
+// is issued as soon as every wave has finished reading tile t's slot (in
+// the middle of k-tile t), so a load has about NSTG - 1 k-tiles of MFMA time
+// to land.  The per-k-tile barrier is fence-free (lds_barrier):
+// __syncthreads() would add s_waitcnt vmcnt(0) and wait for the younger
+// stages too, serialising the ring.  MINB = workgroups per CU the register/LDS budget is sized for
 // (3 for 128x128 tiles, so one workgroup's prologue and epilogue latency
 // overlaps the others' main loops; 1 for the 8-wave 256x256 tile).  NWN =
 // waves along N (2 x NWN waves, each owning a (BM/2) x (BN/NWN) sub-tile).
@@ -359,7 +360,7 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
     static_assert(A_INST * RPD * NW == BM && B_INST * RPD * NW == BN, "DMA split");
     constexpr int STAGE = (BM + BN) * BK;    // halves per LDS buffer
     static_assert(A_INST >= 1 && B_INST >= 1, "tile too small for the DMA split");
-    static_assert(NSTG >= 2 && (NSTG - 2) * (A_INST + B_INST) <= 63, "vmcnt range");
+    static_assert(NSTG >= 2 && (NSTG - 1) * (A_INST + B_INST) <= 63, "vmcnt range");
     __shared__ __attribute__((aligned(16))) half_t lds[NSTG][STAGE];
 
     int tm, tn;
@@ -407,62 +408,68 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
         for (int j = 0; j < NI; ++j) acc[i][j] = f16x{};
 
     const int KT = K / BK;
-    // Prologue: k-tiles 0 .. NSTG-2 (clamped: short K re-fetches the last
-    // tile, keeping the per-stage instruction count fixed for vmcnt).
+    // Prologue: k-tiles 0 .. NSTG-1 fill the ring (clamped: short K
+    // re-fetches the last tile, keeping the per-stage instruction count
+    // fixed for vmcnt).
 #pragma unroll
-    for (int st = 0; st < NSTG - 1; ++st)
+    for (int st = 0; st < NSTG; ++st)
 #pragma unroll
         for (int idx = 0; idx < INST; ++idx) issue_one(idx, min(st, KT - 1) * BK, st);
 
-    // Issue order of one k-tile, pinned with scheduling fences: fragments of
-    // substep kk+1 are read while the MFMAs of kk run, and the DMA of k-tile
-    // kt + NSTG - 1 is spread between MFMA row groups — issued as one burst
-    // it stalls the wave on a full load queue before its first MFMA.
-    constexpr int GROUPS = KK * MI;                      // MFMA row groups per k-tile
-    constexpr int PER_G = (INST + GROUPS - 1) / GROUPS;  // DMA instructions per group
+    // Fragment reads of (k-tile, substep) pairs run one MFMA group ahead of
+    // their use, across k-tile boundaries: the barrier that publishes k-tile
+    // kt + 1 sits before the MFMAs of kt's last substep, so kt + 1's first
+    // fragments are read while those MFMAs run.  After that barrier every
+    // wave has finished reading slot kt % NSTG, which then receives the DMA
+    // of k-tile kt + NSTG.
+    h8 af[KK][MI], bf[KK][NI];
+    auto load_frags = [&](int slot, int kk) {
+        const half_t* As = lds[slot];
+        const half_t* Bs = lds[slot] + BM * BK;
+        const int c = kk * 2 + lhalf;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            const int r = wm * WM + i * 32 + lrow;
+            af[kk][i] = *reinterpret_cast<const h8*>(As + r * BK + ((c ^ chunk_swz<BK>(r)) << 3));
+        }
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int r = wn * WN + j * 32 + lrow;
+            bf[kk][j] = *reinterpret_cast<const h8*>(Bs + r * BK + ((c ^ chunk_swz<BK>(r)) << 3));
+        }
+    };
+    // k-tile 0 has landed once at most the NSTG-1 newer k-tiles remain; in
+    // the loop, k-tile kt + 1 once at most NSTG-2 remain (kt + NSTG is
+    // issued after that wait).
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTG - 1) * INST) : "memory");
+    lds_barrier();
+    load_frags(0, 0);
     for (int kt = 0; kt < KT; ++kt) {
-        // k-tile kt has landed once at most the NSTG-2 newer stages remain.
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTG - 2) * INST) : "memory");
-        lds_barrier();
         const int cur = kt % NSTG;
-        const int nslot = (kt + NSTG - 1) % NSTG;  // the slot consumed at kt - 1
-        // Past the end the DMA re-fetches the last k-tile into a slot that
-        // is never read again (keeps every iteration's count equal).
-        const int knext = min(kt + NSTG - 1, KT - 1) * BK;
-        const half_t* As = lds[cur];
-        const half_t* Bs = lds[cur] + BM * BK;
-        h8 af[KK][MI], bf[KK][NI];
-        auto load_frags = [&](int kk) {
-            const int c = kk * 2 + lhalf;
-#pragma unroll
-            for (int i = 0; i < MI; ++i) {
-                const int r = wm * WM + i * 32 + lrow;
-                af[kk][i] = *reinterpret_cast<const h8*>(As + r * BK + ((c ^ chunk_swz<BK>(r)) << 3));
-            }
-#pragma unroll
-            for (int j = 0; j < NI; ++j) {
-                const int r = wn * WN + j * 32 + lrow;
-                bf[kk][j] = *reinterpret_cast<const h8*>(Bs + r * BK + ((c ^ chunk_swz<BK>(r)) << 3));
-            }
-        };
-        load_frags(0);
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-            if (kk + 1 < KK) load_frags(kk + 1);
+            if (kk + 1 < KK) {
+                load_frags(cur, kk + 1);
+            } else {
+                // Unconditional (also on the last k-tile, where it reads a
+                // stale slot that is never used), so the waits the compiler
+                // places for this substep's fragments see one path only.
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTG - 2) * INST) : "memory");
+                lds_barrier();
+                // Past the end the DMA re-fetches the last k-tile into a slot
+                // that is never read again (keeps every wait count equal).
+                const int knext = min(kt + NSTG, KT - 1) * BK;
+#pragma unroll
+                for (int idx = 0; idx < INST; ++idx) issue_one(idx, knext, cur);
+                load_frags((kt + 1) % NSTG, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < MI; ++i) {
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < NI; ++j)
                     acc[i][j] = mfma32x32x16(bf[kk][j], af[kk][i], acc[i][j]);
-#pragma unroll
-                for (int u = 0; u < PER_G; ++u) {
-                    const int idx = (kk * MI + i) * PER_G + u;
-                    if (idx < INST) issue_one(idx, knext, nslot);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
