@@ -88,15 +88,24 @@ struct EpiRope {
 // EPI and ACT are compile-time (ACT < 0: the runtime `act` argument).
 // Caller: the wave's region is free (after a barrier that follows the last
 // read of the k-loop's tiles).
-template <int MI, int NI, int IP, int EPI, typename OutT, bool TR = false, int ACT = -1>
+// SWZ (with TR): unpadded LDS rows of WN floats, the 16-byte chunk c of row
+// r stored at chunk c ^ (r % (WN / 4)), for callers whose region has no room
+// for the padding; reads stay conflict-free, writes see at most two-way
+// conflicts.
+template <int MI, int NI, int IP, int EPI, typename OutT, bool TR = false, int ACT = -1,
+          bool SWZ = false>
 __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds, int lane,
                                                int row0, int col0, int M, int N,
                                                const float* __restrict__ bias, int act,
                                                const OutT* residual, OutT* out, bool vec,
                                                const EpiRope& rope = EpiRope{}) {
     static_assert(MI % IP == 0, "IP must divide MI");
+    static_assert(!SWZ || TR, "the swizzled layout is for the transposed blocks");
     constexpr int WN = NI * 32;
-    constexpr int LDW = TR ? WN + 4 : WN;  // LDS row stride (floats)
+    constexpr int LDW = TR ? (SWZ ? WN : WN + 4) : WN;  // LDS row stride (floats)
+    constexpr int CMASK = WN / 4 - 1;
+    // Float offset of the 16-byte chunk holding column c (a multiple of 4) of row r.
+    auto at = [&](int r, int c) { return r * LDW + (SWZ ? (((c >> 2) ^ (r & CMASK)) << 2) : c); };
     constexpr int LPR = WN / 4;    // lanes per row
     constexpr int RPI = 64 / LPR;  // rows per iteration
     constexpr int ITERS = IP * 32 / RPI;
@@ -134,9 +143,8 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const f16x& a = acc[p * IP + ii][j];
-                        *reinterpret_cast<f4*>(wlds + (ii * 32 + lrow) * LDW + j * 32 + 8 * g +
-                                               4 * lh) = f4{a[4 * g], a[4 * g + 1], a[4 * g + 2],
-                                                            a[4 * g + 3]};
+                        *reinterpret_cast<f4*>(wlds + at(ii * 32 + lrow, j * 32 + 8 * g + 4 * lh)) =
+                            f4{a[4 * g], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]};
                     }
                 } else {
 #pragma unroll
@@ -233,7 +241,7 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
             f4 v[U];
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                v[u] = *reinterpret_cast<const f4*>(wlds + ((it0 + u) * RPI + rr) * LDW + cq * 4);
+                v[u] = *reinterpret_cast<const f4*>(wlds + at((it0 + u) * RPI + rr, cq * 4));
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const f4 o = finish(v[u], rb[b & 1][u]);
@@ -284,7 +292,7 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
         f4 v[U];
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            v[u] = *reinterpret_cast<const f4*>(wlds + ((it0 + u) * RPI + rr) * LDW + cq * 4);
+            v[u] = *reinterpret_cast<const f4*>(wlds + at((it0 + u) * RPI + rr, cq * 4));
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int grow = batch_row(b, u);

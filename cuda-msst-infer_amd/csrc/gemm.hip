@@ -477,9 +477,12 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
 
     // acc holds the transposed blocks (W_j . A_i^T, see store_tile_lds).
     constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / NW);
-    constexpr int kIP = pick_ip<MI, WN + 4, kRegion>();
-    static_assert(kIP * 32 * (WN + 4) <= kRegion, "epilogue staging does not fit in LDS");
-    store_tile_lds<MI, NI, kIP, EPI, OutT, true, ACT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+    // Padded staging rows when a fragment row of them fits the wave's share
+    // of the ring, else the unpadded swizzled layout.
+    constexpr bool kSwz = 32 * (WN + 4) > kRegion;
+    constexpr int kIP = pick_ip<MI, kSwz ? WN : WN + 4, kRegion>();
+    static_assert(kIP * 32 * (kSwz ? WN : WN + 4) <= kRegion, "epilogue staging does not fit in LDS");
+    store_tile_lds<MI, NI, kIP, EPI, OutT, true, ACT, kSwz>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
                                            lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act,
                                            residual, out, vec != 0, rope);
 }
