@@ -61,25 +61,25 @@ def run_cli(args):
     return r.stdout
 
 
-def separate(tmp_path, cfg, w, audio, mode):
+def separate(tmp_path, cfg, w, audio, mode, extra=()):
     model = tmp_path / "m.csm"
     csm_file.write_csm(model, cfg, w)
     inp = tmp_path / "mix.wav"
     wavfile.write(inp, cfg["sample_rate"], np.ascontiguousarray(audio.T))
     out = tmp_path / f"out_{mode}"
     run_cli(["--model", str(model), "--input", str(inp), "--output", str(out), "--stem", "-1",
-             f"--{mode}"])
+             f"--{mode}", *extra])
     stems = []
     for name in cfg["instruments"]:
         sr, y = wavfile.read(out / f"{name}.wav")
         assert sr == cfg["sample_rate"] and y.dtype == np.float32
-        stems.append(y.T)
+        stems.append(y.T if y.ndim == 2 else y[None])
     return np.stack(stems)  # [stems, ch, S]
 
 
-def oracle_separate(oracle, cfg, w, audio):
+def oracle_separate(oracle, cfg, w, audio, num_overlap=None):
     chunk = cfg["chunk_size"]
-    step = chunk // cfg["num_overlap"]
+    step = chunk // (num_overlap or cfg["num_overlap"])
     model = oracle.melbandroformer_forward if "num_bands" in cfg else oracle.bsroformer_forward
     fwd = lambda b: model(cfg, w, b)
     if audio.shape[1] > chunk:
@@ -144,6 +144,34 @@ def test_cli_melband_unit_mask_returns_the_mix(tmp_path, oracle, cuda, bands):
     y = separate(tmp_path, cfg, w, audio, "fp16")
     for s in range(y.shape[0]):
         assert rel_err(y[s], audio) < 1e-5
+
+
+def test_cli_overlap_override(tmp_path, oracle, cuda):
+    """--overlap 4 (>= 1: the number of overlaps, inference_app.cpp:59-70)
+    cuts chunks every chunk / 4 samples instead of the model's default 2."""
+    rng = np.random.default_rng(11)
+    audio = (0.3 * rng.standard_normal((2, 10000))).astype(np.float32)
+    w = csm_file.bsr_checkpoint(CFG, seed=8)
+    y = separate(tmp_path, CFG, w, audio, "fp32", ("--overlap", "4"))
+    r = oracle_separate(oracle, CFG, w, audio, num_overlap=4)
+    r2 = oracle_separate(oracle, CFG, w, audio)
+    for s in range(y.shape[0]):
+        assert rel_err(y[s], r[s]) < 1e-4, (s, rel_err(y[s], r[s]))
+    assert rel_err(r[0], r2[0]) > 1e-3  # the override changes the result
+
+
+def test_cli_mono_single_stem_melband(tmp_path, oracle, cuda):
+    """A mono, one-stem MelBandRoformer (channel count 1 through the band
+    gather / merge and the WAV path)."""
+    cfg = copy.deepcopy(MBR_CFG)
+    cfg.update(stereo=False, num_stems=1, instruments=["vocals"])
+    _, counts = oracle.mel_bands(cfg["sample_rate"], cfg["stft_n_fft"], cfg["num_bands"], 1)
+    w = csm_file.mbr_checkpoint(cfg, counts, seed=9)
+    audio = (0.3 * np.random.default_rng(12).standard_normal((1, 10000))).astype(np.float32)
+    y = separate(tmp_path, cfg, w, audio, "fp32")
+    r = oracle_separate(oracle, cfg, w, audio)
+    assert y.shape == r.shape == (1, 1, 10000)
+    assert rel_err(y[0], r[0]) < 1e-4
 
 
 def test_cli_unit_mask_returns_the_mix(tmp_path, cuda):
