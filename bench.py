@@ -73,7 +73,9 @@ def attn_flops_chunk(batch):
     return DEPTH * (t + f)
 
 
-def make_weights(torch, seed, dtype):
+def make_weights(torch, seed, dtype, dim=DIM, ff=FF, depth=DEPTH, per_layer_norm=False):
+    """Seeded weights of a 2 * depth transformer stack; per_layer_norm: the
+    MelBandRoformer form (a norm closing every transformer, no final norm)."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     hd = HEADS * DH
 
@@ -81,15 +83,40 @@ def make_weights(torch, seed, dtype):
         return (torch.randn(*s, device="cuda", generator=g) * 0.02).to(dt)
 
     def gm():
-        return 1.0 + torch.randn(DIM, device="cuda", generator=g) * 0.02
+        return 1.0 + torch.randn(dim, device="cuda", generator=g) * 0.02
 
     layers = []
-    for _ in range(2 * DEPTH):
-        layers.append(dict(attn_gamma=gm(), w_qkv=n(3 * hd, DIM), w_gate=n(HEADS, DIM),
-                           b_gate=n(HEADS, dt=torch.float32), w_out=n(DIM, hd), ff_gamma=gm(),
-                           w_ff1=n(FF, DIM), b_ff1=n(FF, dt=torch.float32), w_ff2=n(DIM, FF),
-                           b_ff2=n(DIM, dt=torch.float32)))
-    return layers, gm()
+    for _ in range(2 * depth):
+        lw = dict(attn_gamma=gm(), w_qkv=n(3 * hd, dim), w_gate=n(HEADS, dim),
+                  b_gate=n(HEADS, dt=torch.float32), w_out=n(dim, hd), ff_gamma=gm(),
+                  w_ff1=n(ff, dim), b_ff1=n(ff, dt=torch.float32), w_ff2=n(dim, ff),
+                  b_ff2=n(dim, dt=torch.float32))
+        if per_layer_norm:
+            lw["final_gamma"] = gm()
+        layers.append(lw)
+    return layers, (None if per_layer_norm else gm())
+
+
+def mbr_stack_time(msst, torch, steps):
+    """The MelBandRoformer stack of the same 8 s chunk (depth 6, dim 384,
+    FF 1536, 60 bands, a norm after every transformer), timed like the
+    headline workload; reported beside it, not as the metric."""
+    bands, dim, ff, depth = 60, 384, 1536, 6
+    layers, _ = make_weights(torch, 2, torch.float16, dim, ff, depth, per_layer_norm=True)
+    st = msst.RoformerStack(layers, None, 1, FRAMES, bands, dim, HEADS, DH, ff, msst.F16)
+    x = torch.randn(1, FRAMES, bands, dim, device="cuda",
+                    generator=torch.Generator(device="cuda").manual_seed(3))
+    for _ in range(2):
+        st(x)
+    ms = time_events(torch, lambda: st(x), steps) / steps
+    assert torch.isfinite(x).all().item(), "non-finite MelBandRoformer stack output"
+    M = FRAMES * bands
+    hd = HEADS * DH
+    flops = 2 * depth * M * 2 * (dim * 3 * hd + hd * dim + dim * ff + ff * dim)
+    return {"ms_per_chunk": round(ms, 3), "gemm_flops_per_chunk": flops,
+            "config": "MelBandRoformer stack, one 8 s chunk: depth 6, dim 384, 8 heads x 64, "
+                      "FF 1536 GELU, time layers on [60, 801, 384], frequency layers on "
+                      "[801, 60, 384], a norm after every transformer; fp16 weights"}
 
 
 def time_events(torch, fn, steps):
@@ -439,6 +466,7 @@ def main():
     # Either side of the stack (not part of the timed step): band split and
     # one stem's mask estimator on the same chunk.
     out["bands"] = band_table(msst, torch, B)
+    out["mbr_stack"] = mbr_stack_time(msst, torch, max(2, min(10, args.steps)))
     if not args.no_cpu:
         cpu, parity = cpu_baseline_and_parity(msst, torch, args)
         out["cpu_baseline"] = cpu
