@@ -638,3 +638,38 @@ def test_melbandroformer_forward_unit_mask_returns_input(oracle, precomputed):
     assert y.shape == (1, 2, 2, 64 * 40)
     for s in range(2):
         assert rel_err(y[0, s], x[0]) < 1e-5
+
+
+def test_process_chunked_crossfade_closed_form(oracle):
+    """A model that outputs its chunk's first sample everywhere exposes the
+    windows: on a ramp input, the stitched track between two chunk starts
+    is the weighted mean of two constants, so the linear fades (chunk / 10
+    samples, i / (fade - 1)), the step, the border reflect padding and the
+    untouched first chunk start follow in closed form (inference_app.cpp:
+    100-324).  The identity-model check cannot see any of these."""
+    C, step, S = 1000, 500, 5000
+    fade, border = C // 10, C - step
+    x = np.arange(S, dtype=np.float32)[None]
+    y = oracle.process_chunked(x, C, step, 3, lambda b: np.repeat(b[:, :, :1], C, axis=2))[0]
+    assert y.shape == (S,)
+    r = lambda i: i / (fade - 1)
+    # Chunk starts (padded coordinates) st = 1500 and 2000 carry the values
+    # st - border = 1000 and 1500; they share padded positions [2000, 2500).
+    a, b = 1000.0, 1500.0
+    for p in range(2000, 2500):
+        t = p - border
+        if p < 2000 + fade:          # fade-in of the later chunk
+            w = r(p - 2000)
+            want = (a + w * b) / (1 + w)
+        elif p >= 2500 - fade:       # fade-out of the earlier chunk
+            w = 1 - r(p - (2500 - fade))
+            want = (w * a + b) / (w + 1)
+        else:
+            want = (a + b) / 2
+        assert abs(y[t] - want) <= 1e-3 * abs(want), (t, y[t], want)
+    # Track start: padded chunk 0 holds the reflected x[border] = 500 with
+    # no fade-in; the chunk at st = 500 holds x[0] = 0 and fades in.
+    for t in range(fade):
+        w = r(t)
+        want = 500.0 / (1 + w)
+        assert abs(y[t] - want) <= 1e-3 * want, (t, y[t], want)
