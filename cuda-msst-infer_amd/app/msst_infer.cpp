@@ -89,6 +89,11 @@ int main(int argc, char** argv) {
             return 0;
         }
         const app::AudioData audio = app::load_wav(a.input);
+        // main.cpp:163-166: a rate mismatch is reported, not resampled.
+        if (audio.sample_rate != model.sample_rate)
+            std::cerr << "Warning: audio sample rate (" << audio.sample_rate
+                      << ") != model sample rate (" << model.sample_rate
+                      << "). Results may be incorrect.\n";
         if (audio.channels != model.model->audio_channels())
             throw std::runtime_error("the model expects " +
                                      std::to_string(model.model->audio_channels()) + " channels");
@@ -99,23 +104,30 @@ int main(int argc, char** argv) {
         const std::vector<float> host = out.to_cpu_f32();
         const int64_t frames = out.size(-1);
         const int ch = audio.channels;
-        std::vector<int> stems;
-        if (a.stem < 0)
-            for (int s = 0; s < model.num_sources; ++s) stems.push_back(s);
-        else if (a.stem < model.num_sources)
-            stems.push_back(a.stem);
-        else
-            throw std::runtime_error("stem index out of range");
+        // inference_app.cpp:576-617: a one-source model writes output.wav (or
+        // the given .wav path) whatever --stem says; a multi-source model
+        // writes every stem for -1 or the chosen one, named by its label.
         fs::path out_path(a.output);
-        for (int s : stems) {
-            fs::path file = out_path;
-            if (stems.size() > 1 || out_path.extension() != ".wav") {
-                fs::create_directories(out_path);
-                file = out_path / (model.stem_names[(size_t)s] + ".wav");
-            }
+        auto target = [&](const std::string& name) {
+            if (out_path.extension() == ".wav") return out_path;
+            fs::create_directories(out_path);
+            return out_path / (name + ".wav");
+        };
+        auto write = [&](int s, const fs::path& file) {
             app::save_wav(file.string(), host.data() + (size_t)s * ch * frames, ch, frames,
                           model.sample_rate);
             std::cout << "wrote " << file.string() << "\n";
+        };
+        if (model.num_sources == 1) {
+            write(0, target("output"));
+        } else if (a.stem >= 0 && a.stem < model.num_sources) {
+            write(a.stem, target(model.stem_names[(size_t)a.stem]));
+        } else if (a.stem == -1) {
+            fs::create_directories(out_path);
+            for (int s = 0; s < model.num_sources; ++s)
+                write(s, out_path / (model.stem_names[(size_t)s] + ".wav"));
+        } else {
+            throw std::runtime_error("Stem index out of range");
         }
         std::cout << "inference " << ms << " ms for " << audio.frames << " samples x " << ch
                   << " channels\n";

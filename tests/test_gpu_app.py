@@ -70,7 +70,9 @@ def separate(tmp_path, cfg, w, audio, mode, extra=()):
     run_cli(["--model", str(model), "--input", str(inp), "--output", str(out), "--stem", "-1",
              f"--{mode}", *extra])
     stems = []
-    for name in cfg["instruments"]:
+    # A one-source model writes output.wav (inference_app.cpp:609-616).
+    names = cfg["instruments"] if cfg["num_stems"] > 1 else ["output"]
+    for name in names:
         sr, y = wavfile.read(out / f"{name}.wav")
         assert sr == cfg["sample_rate"] and y.dtype == np.float32
         stems.append(y.T if y.ndim == 2 else y[None])
@@ -205,3 +207,15 @@ def test_cli_list_stems_and_errors(tmp_path, cuda):
     r = subprocess.run([CLI, "--model", str(mdx), "--list-stems"], capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 1 and "MDX23C checkpoints are not supported" in r.stderr
+    wav = tmp_path / "mix.wav"
+    wavfile.write(wav, 44100, np.zeros((3000, 2), np.float32))
+    r = subprocess.run([CLI, "--model", str(model), "--input", str(wav), "--output",
+                        str(tmp_path / "o"), "--stem", "5"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 1 and "Stem index out of range" in r.stderr
+    # One chosen stem into an explicit .wav path; a rate mismatch only warns.
+    wavfile.write(wav, 48000, np.zeros((3000, 2), np.float32))
+    target = tmp_path / "single.wav"
+    r = subprocess.run([CLI, "--model", str(model), "--input", str(wav), "--output", str(target),
+                        "--stem", "1"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and target.exists() and "sample rate" in r.stderr
