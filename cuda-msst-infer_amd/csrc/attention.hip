@@ -387,16 +387,6 @@ __device__ __forceinline__ float pair_sum(float a) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// A pointer the compiler can keep in SGPRs (the value is wave-uniform by
-// construction; without this, a descriptor built from it is waterfalled).
-template <typename T>
-__device__ __forceinline__ const T* uniform_ptr(const T* q) {
-    const uint64_t v = reinterpret_cast<uint64_t>(q);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
-}
-
 constexpr float kRescaleLog2 = 8.0f;
 
 template <int HPW>

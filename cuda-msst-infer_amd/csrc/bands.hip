@@ -305,10 +305,15 @@ __global__ __launch_bounds__(kGemmThreads, 3) void band_gemm_kernel(BandGemmArgs
     // Epilogue: acc[i][j] = W_j . A_i^T, so register 4 g + e of lane l is row
     // l % 32, column 8 g + 4 (l / 32) + e of block (i, j).  Each 32-row
     // fragment row goes through the wave's LDS region (rows padded by 4
-    // floats) and is read back as 4 consecutive columns per lane.
+    // floats) and is read back as 4 consecutive columns per lane.  Stores go
+    // through a buffer resource based at the wave's first row, with the
+    // offset of an invalid row or column replaced by one past the resource
+    // (the hardware drops the store): no per-row branch, so the compiler's
+    // waits are exact instead of one full memory round trip per store.
     constexpr int LDW = WN + 4;
     constexpr int LPR = WN / 4;      // lanes per row (16)
     constexpr int RPI = 64 / LPR;    // rows per read (4)
+    constexpr int ROWS = 32 / RPI;   // reads per fragment row (8)
     float* wl = reinterpret_cast<float*>(&lds[0][0]) + wid * (32 * LDW);
     static_assert(4 * 32 * LDW * 4 <= (int)sizeof(lds), "epilogue staging does not fit");
     const int rr = lane / LPR, cq = lane % LPR;
@@ -320,6 +325,28 @@ __global__ __launch_bounds__(kGemmThreads, 3) void band_gemm_kernel(BandGemmArgs
         if constexpr (MODE == kGlu) c = (c >> 1) + (c & 1) * glu_d;
         bv[e] = bias[c];
     }
+    const int wrow = __builtin_amdgcn_readfirstlane(m0 + wm * WM);
+    const int nrows = max(0, min(M - wrow, WM));
+    // Base (element) of the wave's first row in the band's output columns.
+    int64_t base;
+    int esize;
+    if constexpr (MODE == kSplit) {
+        base = (int64_t)wrow * args.ldo + b * plan->dim;
+        esize = 4;
+    } else if constexpr (MODE == kHidden) {
+        base = (int64_t)b * args.o_band + (int64_t)wrow * args.ldo;
+        esize = 2;
+    } else {
+        base = (int64_t)wrow * args.ldo + plan->foff[b];
+        esize = 4;
+    }
+    char* const obase = uniform_ptr(reinterpret_cast<char*>(args.out) + base * esize);
+    // The resource spans the wave's rows below M (whole output rows).
+    const int span = __builtin_amdgcn_readfirstlane(nrows * args.ldo * esize);
+    const __amdgpu_buffer_rsrc_t ro =
+        __builtin_amdgcn_make_buffer_rsrc(obase, (short)0, span, 0x00020000);
+    const uint32_t kDrop = 0x80000000u;  // past any resource here (span < 2^31)
+    const bool col_ok = col < N;
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
 #pragma unroll
@@ -329,37 +356,33 @@ __global__ __launch_bounds__(kGemmThreads, 3) void band_gemm_kernel(BandGemmArgs
                 *reinterpret_cast<f4*>(wl + lrow * LDW + j * 32 + 8 * g + 4 * lhalf) =
                     f4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                        acc[i][j][4 * g + 3]};
+        f4 v[ROWS];
 #pragma unroll
-        for (int it = 0; it < 32 / RPI; ++it) {
-            const int lr = it * RPI + rr;
-            const int grow = m0 + wm * WM + i * 32 + lr;
-            const f4 v = *reinterpret_cast<const f4*>(wl + lr * LDW + cq * 4) + bv;
-            if (grow < M && col < N) {
-                if constexpr (MODE == kSplit) {
-                    // N = dim is a multiple of 4: the 4 columns are valid together.
-                    float* o = reinterpret_cast<float*>(args.out) + (int64_t)grow * args.ldo +
-                               b * plan->dim + col;
-                    *reinterpret_cast<f4*>(o) = v;
-                } else if constexpr (MODE == kHidden) {
-                    half_t* o = reinterpret_cast<half_t*>(args.out) + (int64_t)b * args.o_band +
-                                (int64_t)grow * args.ldo + col;
-                    *reinterpret_cast<h4*>(o) =
-                        h4{(half_t)tanh_fast(v[0]), (half_t)tanh_fast(v[1]),
-                           (half_t)tanh_fast(v[2]), (half_t)tanh_fast(v[3])};
-                } else {
-                    // Columns (col, col + 1) and (col + 2, col + 3) are GLU
-                    // pairs m = col / 2, col / 2 + 1 (N = 2 d is even and col
-                    // is a multiple of 4, so a lane's pairs are whole).
-                    float* o = reinterpret_cast<float*>(args.out) + (int64_t)grow * args.ldo +
-                               plan->foff[b] + (col >> 1);
-                    const float g0 = v[0] * (1.0f / (1.0f + expf(-v[1])));
-                    if (col + 2 < N) {
-                        const float g1 = v[2] * (1.0f / (1.0f + expf(-v[3])));
-                        *reinterpret_cast<float2*>(o) = float2{g0, g1};
-                    } else {
-                        o[0] = g0;
-                    }
-                }
+        for (int it = 0; it < ROWS; ++it)
+            v[it] = *reinterpret_cast<const f4*>(wl + (it * RPI + rr) * LDW + cq * 4) + bv;
+#pragma unroll
+        for (int it = 0; it < ROWS; ++it) {
+            const int lr = i * 32 + it * RPI + rr;  // row within the wave tile
+            const bool ok = col_ok && lr < nrows;
+            if constexpr (MODE == kSplit) {
+                // N = dim is a multiple of 4: the 4 columns are valid together.
+                const uint32_t off = ok ? (uint32_t)((lr * args.ldo + col) * 4) : kDrop;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, v[it]), ro, off, 0, 0);
+            } else if constexpr (MODE == kHidden) {
+                const uint32_t off = ok ? (uint32_t)((lr * args.ldo + col) * 2) : kDrop;
+                const h4 h = h4{(half_t)tanh_fast(v[it][0]), (half_t)tanh_fast(v[it][1]),
+                                (half_t)tanh_fast(v[it][2]), (half_t)tanh_fast(v[it][3])};
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, h), ro, off, 0, 0);
+            } else {
+                // Columns (col, col + 1) and (col + 2, col + 3) are GLU pairs
+                // m = col / 2, col / 2 + 1 (N = 2 d is even and col is a
+                // multiple of 4, so a lane's pairs are whole).
+                const float g0 = v[it][0] * (1.0f / (1.0f + expf(-v[it][1])));
+                const float g1 = v[it][2] * (1.0f / (1.0f + expf(-v[it][3])));
+                const uint32_t off = ok ? (uint32_t)((lr * args.ldo + (col >> 1)) * 4) : kDrop;
+                const uint32_t off1 = (ok && col + 2 < N) ? off + 4u : kDrop;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(g0), ro, off, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(g1), ro, off1, 0, 0);
             }
         }
     }

@@ -35,16 +35,6 @@ constexpr int pick_ip() {
     return ip;
 }
 
-// A wave-uniform pointer held in SGPRs (buffer resources built from it need
-// no per-lane loop).
-template <typename T>
-__device__ __forceinline__ T* uniform_ptr(T* p) {
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
-}
-
 // Epilogue variants of store_tile_lds.
 constexpr int kEpiPlain = 0;  // act(acc + bias)
 constexpr int kEpiRes = 1;    // act(acc + bias) + residual

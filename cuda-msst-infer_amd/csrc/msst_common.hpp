@@ -140,6 +140,17 @@ __device__ __forceinline__ void dma16(const void* base, int bytes, lds_half_t* l
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voffset, 0, 0, 0);
 }
 
+// A pointer the compiler can keep in SGPRs (the value is wave-uniform by
+// construction; without this, a buffer descriptor built from it is
+// waterfalled, one loop iteration per distinct lane value).
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
 // Workgroup barrier for LDS hand-offs only.  __syncthreads() carries a
 // workgroup release/acquire fence, which the compiler lowers to
 // s_waitcnt vmcnt(0) before s_barrier: it waits for every outstanding
