@@ -179,6 +179,23 @@ __device__ __forceinline__ int divmod24(int n, int d, float inv_d, int& r) {
 }
 
 // Butterfly sum over the 64 lanes of a wave.
+// Sum over the 64 lanes with DPP lane moves (no LDS round trips): butterfly
+// within quads, mirrors within 8- and 16-lane rows, then the row broadcasts
+// carry rows 0-2 into lane 63, which is read back as a wave-uniform value.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_move(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float dpp_wave_sum(float v) {
+    v += dpp_move<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v += dpp_move<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v += dpp_move<0x141, 0xF>(v);  // row_half_mirror
+    v += dpp_move<0x140, 0xF>(v);  // row_mirror
+    v += dpp_move<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_move<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);

@@ -147,7 +147,9 @@ __global__ __launch_bounds__(kThreads) void rms_norm_gate_h_kernel(
     half_t* __restrict__ out, const half_t* __restrict__ wg, const float* __restrict__ bg,
     float* __restrict__ gates, int64_t rows, int D, int G) {
     const int lane = threadIdx.x & 63;
-    const int64_t wave0 = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    // Wave-uniform (readfirstlane), so the per-row buffer resources stay in SGPRs.
+    const int64_t wave0 =
+        (int64_t)blockIdx.x * kRowsPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t nwaves = (int64_t)gridDim.x * kRowsPerBlock;
     if (wave0 >= rows) return;
     f4 gm[NS];
@@ -165,37 +167,55 @@ __global__ __launch_bounds__(kThreads) void rms_norm_gate_h_kernel(
             wr[i][g][1] = h2{w[2], w[3]};
         }
     }
-    f4 v[NS];
+    // Every global access goes through a per-row buffer resource: rows past
+    // the end and columns past D read zero / drop their stores in hardware,
+    // so the loop has no data-dependent branch and the compiler's waits
+    // cover only the data each step needs (with branches it waited for the
+    // prefetched row right after issuing it).  Cross-lane sums use DPP moves
+    // (dpp_wave_sum): the gate sums of all G heads end wave-uniform, and
+    // lane g < G finishes and stores gate g.
+    const uint32_t kDrop = 0x80000000u;
+    uint32_t xoff[NS], ooff[NS];
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
         const int j = 4 * (64 * i + lane);
-        v[i] = j < D ? load4<XT>(x + wave0 * D + j) : f4{0.0f, 0.0f, 0.0f, 0.0f};
+        xoff[i] = j < D ? (uint32_t)(j * (int)sizeof(XT)) : kDrop;
+        ooff[i] = j < D ? (uint32_t)(j * 2) : kDrop;
     }
-    for (int64_t row = wave0; row < rows; row += nwaves) {
-        const int64_t nxt = row + nwaves;
-        f4 vn[NS];
+    const float bgl = lane < G ? bg[lane] : 0.0f;
+    const uint32_t goff = lane < G ? (uint32_t)(lane * 4) : kDrop;
+    auto load_row = [&](int64_t r, f4 (&dst)[NS]) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<XT*>(x) + (r < rows ? r : 0) * D, (short)0,
+            r < rows ? D * (int)sizeof(XT) : 0, 0x00020000);
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
-            const int j = 4 * (64 * i + lane);
-            vn[i] = (nxt < rows && j < D) ? load4<XT>(x + nxt * D + j)
-                                          : f4{0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (std::is_same<XT, float>::value) {
+                dst[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, xoff[i], 0, 0));
+            } else {
+                const h4 hv = __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rs, xoff[i], 0, 0));
+                dst[i] = f4{(float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]};
+            }
         }
+    };
+    auto process = [&](int64_t row, const f4 (&v)[NS]) {
         float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < NS; ++i)
             ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
-        ss = wave_sum(ss);
-        const float inv = 1.0f / sqrtf(ss + 1e-12f);
+        const float inv = 1.0f / sqrtf(dpp_wave_sum(ss) + 1e-12f);
         float gacc[GP];
 #pragma unroll
         for (int g = 0; g < GP; ++g) gacc[g] = 0.0f;
+        const bool live = row < rows;  // a row past the end computes on zeros, stores nothing
+        const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+            out + (live ? row : 0) * D, (short)0, live ? D * 2 : 0, 0x00020000);
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
-            const int j = 4 * (64 * i + lane);
             h4 y;
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = (half_t)(v[i][e] * inv * gm[i][e] * scale);
-            if (j < D) *reinterpret_cast<h4*>(out + row * D + j) = y;
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, y), ro, ooff[i], 0, 0);
             const h2 y0 = h2{y[0], y[1]}, y1 = h2{y[2], y[3]};
 #pragma unroll
             for (int g = 0; g < GP; ++g) {
@@ -203,13 +223,31 @@ __global__ __launch_bounds__(kThreads) void rms_norm_gate_h_kernel(
                 gacc[g] = __builtin_amdgcn_fdot2(y1, wr[i][g][1], gacc[g], false);
             }
         }
-        float sg = reduce_scatter<GP>(gacc, lane);
-        constexpr int SHIFT = GP == 16 ? 2 : 3;
-        const int g = lane >> SHIFT;
-        if ((lane & ((1 << SHIFT) - 1)) == 0 && g < G)
-            gates[row * G + g] = 1.0f / (1.0f + expf(-(sg + bg[g])));
+        float mine = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NS; ++i) v[i] = vn[i];
+        for (int g = 0; g < GP; ++g) {
+            const float tot = dpp_wave_sum(gacc[g]);
+            mine = lane == g ? tot : mine;
+        }
+        const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+            gates + (live ? row : 0) * G, (short)0, live ? G * 4 : 0, 0x00020000);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(1.0f / (1.0f + expf(-(mine + bgl)))),
+                                              rg, goff, 0, 0);
+    };
+    // Two row buffers in turn: one row is processed while the next loads.
+    // Both halves run unconditionally (the second may be a row past the
+    // end): a branch between them lets the compiler sink the load of the
+    // second row next to its use.  The scheduling fences keep each load
+    // ahead of the other row's work.
+    f4 va[NS], vb[NS];
+    load_row(wave0, va);
+    for (int64_t row = wave0; row < rows; row += 2 * nwaves) {
+        load_row(row + nwaves, vb);
+        __builtin_amdgcn_sched_barrier(0);
+        process(row, va);
+        load_row(row + 2 * nwaves, va);
+        __builtin_amdgcn_sched_barrier(0);
+        process(row + nwaves, vb);
     }
 }
 
