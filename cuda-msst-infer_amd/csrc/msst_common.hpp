@@ -196,11 +196,8 @@ __device__ __forceinline__ float dpp_wave_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
+// Sum over the wave, the same value in every lane (all 64 lanes active).
+__device__ __forceinline__ float wave_sum(float v) { return dpp_wave_sum(v); }
 
 // ---------------------------------------------------------------------------
 // Host-side status helpers.
