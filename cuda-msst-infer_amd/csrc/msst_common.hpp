@@ -47,27 +47,33 @@ __device__ __forceinline__ f16x mfma32x32x2f32(float a, float b, f16x c) {
 
 // ---------------------------------------------------------------------------
 // Epilogue activations.
-// GELU(v) = v/2 (1 + erf(v / sqrt 2)) with erf from Abramowitz & Stegun,
-// Handbook of Mathematical Functions (1964), formula 7.1.26:
-//   erf(z) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),
-//   t = 1 / (1 + p z), z >= 0,  |error| <= 1.5e-7,
-// odd extension for z < 0.  Sixteen VALU operations (v_rcp_f32 and
-// v_exp_f32 among them) against several times that for the library erff,
-// which dominated the FF1 epilogue; 1.5e-7 absolute is far below the fp16
-// output rounding and the 1e-4 fp32 tolerance.
+// GELU(v) = v Phi(v), Phi(v) = (1 + erf(v / sqrt 2)) / 2, with erf from
+// Abramowitz & Stegun, Handbook of Mathematical Functions (1964), formula
+// 7.1.26:
+//   1 - erf(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),
+//   t = 1 / (1 + p z), z >= 0,  |error| <= 1.5e-7.
+// With c = (1 - erf(|v| / sqrt 2)) / 2 (the polynomial's coefficients
+// halved, p folded with 1 / sqrt 2), v Phi(v) is v - v c for v >= 0 and
+// v c = -|v| c for v < 0: both are max(v, 0) - |v| c.  Thirteen VALU
+// operations (v_rcp_f32 and v_exp_f32 among them) against several times
+// that for the library erff, which dominated the FF1 epilogue; there is no
+// cancellation in 1 + erf for negative v, and the 0.75e-7 |v| absolute
+// error is far below the fp16 output rounding and the 1e-4 fp32 tolerance.
+// |v| is capped in the last product so that v = +inf gives +inf (c is 0
+// there), not inf * 0.
 // sigmoid / SiLU use the ROCm device-library expf.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float erf_as7126(float z) {
-    const float a = fabsf(z);
-    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, a, 1.0f));
-    float poly = fmaf(t, 1.061405429f, -1.453152027f);
-    poly = fmaf(t, poly, 1.421413741f);
-    poly = fmaf(t, poly, -0.284496736f);
-    poly = fmaf(t, poly, 0.254829592f);
-    poly *= t;
-    // exp(-a^2) = 2^(-a^2 log2 e); v_exp_f32 flushes to 0 far out.
-    const float e = __builtin_amdgcn_exp2f(-(a * a) * 1.4426950408889634f);
-    return copysignf(fmaf(-poly, e, 1.0f), z);
+__device__ __forceinline__ float gelu_erf(float v) {
+    const float a = fabsf(v);
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752f, a, 1.0f));
+    float p = fmaf(t, 0.5f * 1.061405429f, 0.5f * -1.453152027f);
+    p = fmaf(t, p, 0.5f * 1.421413741f);
+    p = fmaf(t, p, 0.5f * -0.284496736f);
+    p = fmaf(t, p, 0.5f * 0.254829592f);
+    // exp(-v^2 / 2) = 2^(-v^2 log2(e) / 2); v_exp_f32 flushes to 0 far out.
+    const float e = __builtin_amdgcn_exp2f(v * (v * -0.72134752044448170f));
+    const float c = (p * t) * e;
+    return fmaf(-fminf(a, 3.0e38f), c, fmaxf(v, 0.0f));
 }
 
 // tanh(x) = (e^2x - 1) / (e^2x + 1) with e^2x from v_exp_f32 (|x| clamped to
@@ -90,7 +96,7 @@ __device__ __forceinline__ float tanh_fast(float x) {
 template <int ACT>
 __device__ __forceinline__ float act_fixed(float v) {
     if constexpr (ACT == MSST_ACT_GELU)
-        return 0.5f * v * (1.0f + erf_as7126(v * 0.70710678118654752f));
+        return gelu_erf(v);
     else if constexpr (ACT == MSST_ACT_SIGMOID)
         return 1.0f / (1.0f + expf(-v));
     else if constexpr (ACT == MSST_ACT_SILU)

@@ -128,6 +128,50 @@ def test_gelu_error_bound(msst, cuda, wd):
     assert np.all(np.abs(y16 - exact) <= bound + half_ulp)
 
 
+# Launches past one round of workgroups on 256 CUs (one 256 x 256 tile per
+# CU for N = 512, two 256 x 128 tiles for N = 384), with a partly filled
+# last round: in-place residual, bit-identical repeats, and a smaller launch
+# right after.  Reference: float32 BLAS on the same fp16-exact operands.
+LARGE_SHAPES = [(40000, 512, 512), (40000, 2048, 512), (49662, 2048, 512), (48060, 1536, 384),
+             (48060, 384, 384)]
+
+
+def _large_case(M, K, N, seed):
+    rng = np.random.default_rng(seed)
+    x = r16(rng.standard_normal((M, K), dtype=np.float32))
+    w = r16(rng.standard_normal((N, K), dtype=np.float32) * 0.02)
+    b = rng.standard_normal(N, dtype=np.float32) * 0.02
+    res = rng.standard_normal((M, N), dtype=np.float32)
+    return x, w, b, res
+
+
+@pytest.mark.parametrize("M,K,N", LARGE_SHAPES)
+def test_linear_large_residual(msst, cuda, M, K, N):
+    x, w, b, res = _large_case(M, K, N, M + K + N)
+    ref = x @ w.T + b + res
+    xd, wd, bd = dev(x, torch.float16), dev(w, torch.float16), dev(b)
+    outs = []
+    for _ in range(2):
+        xr = dev(res)
+        msst.linear(xd, wd, bd, "none", residual=xr, out=xr)
+        outs.append(host(xr))
+    assert rel_err(outs[0], ref) < TOL_F32
+    assert np.array_equal(outs[0], outs[1])
+    M2 = M - 3001
+    xr2 = dev(res[:M2])
+    msst.linear(xd[:M2], wd, bd, "none", residual=xr2, out=xr2)
+    assert rel_err(host(xr2), ref[:M2]) < TOL_F32
+
+
+@pytest.mark.parametrize("M,K,N", [(40000, 512, 512), (48060, 1536, 384)])
+def test_linear_large_plain_f16(msst, cuda, M, K, N):
+    x, w, b, _ = _large_case(M, K, N, 7 * M + K)
+    ref = x @ w.T + b
+    y = msst.linear(dev(x, torch.float16), dev(w, torch.float16), dev(b), "none",
+                    out_dtype=torch.float16)
+    assert rel_err(host(y), ref) < TOL_F16
+
+
 @pytest.mark.parametrize("wd", ["f16", "f32"])
 def test_linear_residual_in_place(msst, oracle, cuda, wd):
     rng = np.random.default_rng(5)
