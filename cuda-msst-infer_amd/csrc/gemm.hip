@@ -407,6 +407,41 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
 #pragma unroll
         for (int j = 0; j < NI; ++j) acc[i][j] = f16x{};
 
+    // fp32 residual with whole-width wave tiles: the accumulators start from
+    // the residual, read here ahead of the ring's first k-tiles, and the
+    // epilogue only adds the bias and stores.  The residual read then
+    // overlaps the main loop instead of joining the epilogue's write burst,
+    // when every tile of a round finishes at once.  Registers hold rows of
+    // the transposed blocks: row lrow + 32 i, columns 8 g + 4 h .. + 3 of
+    // block j (the MFMA output layout); rows past M read zero.
+    // The loads are unconditional (a wave that keeps the residual for its
+    // epilogue gets an empty resource and reads zeros): a branch here would
+    // make the compiler wait for the whole prologue before the first MFMA.
+    // One workgroup per CU only: at two per CU (the 256 x 128 tiles) the
+    // stack measured slower with it (MelBandRoformer 6.14 -> 6.22 ms per
+    // chunk), against 15.53 -> 15.44 for the 256 x 256 BSRoformer stack.
+    constexpr bool kResInAcc = EPI == kEpiRes && std::is_same<OutT, float>::value && MINB == 1;
+    bool res_in_acc = false;
+    if constexpr (kResInAcc) {
+        res_in_acc = vec != 0 && n0 + wn * WN + WN <= N;
+        const int wrow0 = __builtin_amdgcn_readfirstlane(m0 + wm * WM);
+        const int nrows = res_in_acc ? max(0, min(M - wrow0, WM)) : 0;
+        const float* rbase = uniform_ptr(reinterpret_cast<const float*>(residual) +
+                                         (int64_t)max(wrow0, 0) * N);
+        const int rbytes = __builtin_amdgcn_readfirstlane(nrows * N * 4);
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int c = n0 + wn * WN + j * 32 + 8 * g + 4 * lhalf;
+                    const f4 r = load16_bounded(rbase, rbytes, ((i * 32 + lrow) * N + c) * 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] = r[e];
+                }
+    }
+
     const int KT = K / BK;
     // Prologue: k-tiles 0 .. NSTG-1 fill the ring (clamped: short K
     // re-fetches the last tile, keeping the per-stage instruction count
@@ -415,6 +450,15 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
     for (int st = 0; st < NSTG; ++st)
 #pragma unroll
         for (int idx = 0; idx < INST; ++idx) issue_one(idx, min(st, KT - 1) * BK, st);
+    if constexpr (kResInAcc) {
+        // Take the residual here, behind the ring's DMAs in the vmcnt queue:
+        // the compiler's wait is then vmcnt(stages * instructions) instead of
+        // vmcnt(0) at the main loop's entry.
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) use_now(acc[i][j]);
+    }
 
     // Fragment reads of (k-tile, substep) pairs run one MFMA group ahead of
     // their use, across k-tile boundaries: the barrier that publishes k-tile
@@ -482,6 +526,14 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
     constexpr bool kSwz = 32 * (WN + 4) > kRegion;
     constexpr int kIP = pick_ip<MI, kSwz ? WN : WN + 4, kRegion>();
     static_assert(kIP * 32 * (kSwz ? WN : WN + 4) <= kRegion, "epilogue staging does not fit in LDS");
+    if constexpr (kResInAcc) {
+        if (res_in_acc) {
+            store_tile_lds<MI, NI, kIP, kEpiPlain, OutT, true, ACT, kSwz>(
+                acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion, lane, m0 + wm * WM,
+                n0 + wn * WN, M, N, bias, act, nullptr, out, vec != 0, rope);
+            return;
+        }
+    }
     store_tile_lds<MI, NI, kIP, EPI, OutT, true, ACT, kSwz>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
                                            lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act,
                                            residual, out, vec != 0, rope);

@@ -146,6 +146,17 @@ __device__ __forceinline__ void dma16(const void* base, int bytes, lds_half_t* l
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds, 16, voffset, 0, 0, 0);
 }
 
+// 16 bytes at byte offset off of [base, base + bytes); zeros past the end.
+__device__ __forceinline__ f4 load16_bounded(const float* base, int bytes, uint32_t off) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, bytes, 0x00020000);
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+}
+
+// Makes the compiler complete whatever produces v (a load: its s_waitcnt)
+// at this point of the program, with no instruction of its own.
+__device__ __forceinline__ void use_now(const f16x& v) { asm volatile("" ::"v"(v)); }
+
 // A pointer the compiler can keep in SGPRs (the value is wave-uniform by
 // construction; without this, a buffer descriptor built from it is
 // waterfalled, one loop iteration per distinct lane value).
