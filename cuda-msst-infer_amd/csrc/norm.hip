@@ -74,6 +74,38 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[GP], int lane) {
     return s;
 }
 
+// Eight per-lane partial sums (one per gate) reduced over the wave, with the
+// sum of gate g left in the eight lanes 8g .. 8g + 7.  Each step halves the
+// values a lane carries: the xor-32 and xor-16 exchanges pair two registers
+// through v_permlane32_swap / v_permlane16_swap (no selects needed), the
+// xor-8 one picks by lane bit 3 and moves by DPP row_ror:8; the last three
+// lane bits are summed with DPP (quad perms, row_half_mirror).  21 VALU
+// operations against 8 full wave sums.
+__device__ __forceinline__ float gate_sums8(const float (&v)[8], int lane) {
+    float c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // lane bit 5: values i (clear) / i + 4 (set)
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]),
+                                                        false, false);
+        c[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    float d[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // lane bit 4: + 0 / + 2
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(c[i]), __float_as_uint(c[i + 2]),
+                                                        false, false);
+        d[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const bool b3 = (lane & 8) != 0;  // lane bit 3: + 0 / + 1
+    const float keep = b3 ? d[1] : d[0];
+    const float send = b3 ? d[0] : d[1];
+    float s = keep + dpp_move<0x128, 0xF>(send);  // row_ror:8 = lane ^ 8 within a row
+    s += dpp_move<0xB1, 0xF>(s);   // quad_perm [1,0,3,2]
+    s += dpp_move<0x4E, 0xF>(s);   // quad_perm [2,3,0,1]
+    s += dpp_move<0x141, 0xF>(s);  // row_half_mirror
+    return s;
+}
+
 template <typename XT, typename OutT, typename WT, int GP>
 __global__ __launch_bounds__(kThreads) void rms_norm_vec_kernel(
     const XT* __restrict__ x, const float* __restrict__ gamma, float scale,
@@ -182,8 +214,11 @@ __global__ __launch_bounds__(kThreads) void rms_norm_gate_h_kernel(
         xoff[i] = j < D ? (uint32_t)(j * (int)sizeof(XT)) : kDrop;
         ooff[i] = j < D ? (uint32_t)(j * 2) : kDrop;
     }
-    const float bgl = lane < G ? bg[lane] : 0.0f;
-    const uint32_t goff = lane < G ? (uint32_t)(lane * 4) : kDrop;
+    // GP == 8: gate g is finished in lanes 8g .. 8g + 7 and stored by lane 8g.
+    const int gl = GP == 8 ? lane >> 3 : lane;
+    const bool gstore = GP == 8 ? ((lane & 7) == 0 && gl < G) : lane < G;
+    const float bgl = gl < G ? bg[gl] : 0.0f;
+    const uint32_t goff = gstore ? (uint32_t)(gl * 4) : kDrop;
     auto load_row = [&](int64_t r, f4 (&dst)[NS]) {
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<XT*>(x) + (r < rows ? r : 0) * D, (short)0,
@@ -224,10 +259,14 @@ __global__ __launch_bounds__(kThreads) void rms_norm_gate_h_kernel(
             }
         }
         float mine = 0.0f;
+        if constexpr (GP == 8) {
+            mine = gate_sums8(gacc, lane);
+        } else {
 #pragma unroll
-        for (int g = 0; g < GP; ++g) {
-            const float tot = dpp_wave_sum(gacc[g]);
-            mine = lane == g ? tot : mine;
+            for (int g = 0; g < GP; ++g) {
+                const float tot = dpp_wave_sum(gacc[g]);
+                mine = lane == g ? tot : mine;
+            }
         }
         const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
             gates + (live ? row : 0) * G, (short)0, live ? G * 4 : 0, 0x00020000);
