@@ -82,8 +82,9 @@ struct EpiRope {
 // r stored at chunk c ^ (r % (WN / 4)), for callers whose region has no room
 // for the padding; reads stay conflict-free, writes see at most two-way
 // conflicts.
+// NOBIAS: the accumulators already hold the bias (no add here).
 template <int MI, int NI, int IP, int EPI, typename OutT, bool TR = false, int ACT = -1,
-          bool SWZ = false>
+          bool SWZ = false, bool NOBIAS = false>
 __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds, int lane,
                                                int row0, int col0, int M, int N,
                                                const float* __restrict__ bias, int act,
@@ -150,7 +151,7 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             if constexpr (ACT >= 0)
-                o[e] = act_fixed<ACT>(v[e] + bv[e]);
+                o[e] = act_fixed<ACT>(NOBIAS ? v[e] : v[e] + bv[e]);
             else
                 o[e] = act_apply(v[e] + bv[e], act);
         }

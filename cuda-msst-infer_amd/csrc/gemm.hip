@@ -442,6 +442,26 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
                 }
     }
 
+    // Activation epilogues (FF1): the accumulators start from the bias, so
+    // the VALU-bound epilogue has one operation less per element (columns
+    // past N, or no bias: zeros).
+    constexpr bool kBiasInAcc = EPI == kEpiPlain && ACT != MSST_ACT_NONE;
+    if constexpr (kBiasInAcc) {
+        const float* bb = uniform_ptr(bias);
+        const int bbytes = bias ? N * 4 : 0;
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int c = n0 + wn * WN + j * 32 + 8 * g + 4 * lhalf;
+                const f4 b = load16_bounded(bb, bbytes, (uint32_t)c * 4u);
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] = b[e];
+            }
+    }
+
     const int KT = K / BK;
     // Prologue: k-tiles 0 .. NSTG-1 fill the ring (clamped: short K
     // re-fetches the last tile, keeping the per-stage instruction count
@@ -450,8 +470,8 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
     for (int st = 0; st < NSTG; ++st)
 #pragma unroll
         for (int idx = 0; idx < INST; ++idx) issue_one(idx, min(st, KT - 1) * BK, st);
-    if constexpr (kResInAcc) {
-        // Take the residual here, behind the ring's DMAs in the vmcnt queue:
+    if constexpr (kResInAcc || kBiasInAcc) {
+        // Take the residual / bias here, behind the ring's DMAs in the vmcnt queue:
         // the compiler's wait is then vmcnt(stages * instructions) instead of
         // vmcnt(0) at the main loop's entry.
 #pragma unroll
@@ -534,7 +554,7 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
             return;
         }
     }
-    store_tile_lds<MI, NI, kIP, EPI, OutT, true, ACT, kSwz>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+    store_tile_lds<MI, NI, kIP, EPI, OutT, true, ACT, kSwz, kBiasInAcc>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
                                            lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act,
                                            residual, out, vec != 0, rope);
 }
@@ -759,13 +779,18 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
             // dim 384) takes 256 x 128 tiles at two workgroups per CU instead
             // of padding a quarter of the 256-wide tiles (out-proj / FF2
             // 9-10 % faster).
-            if (act != MSST_ACT_NONE)
+            // (The activation kernels start their accumulators from 16-byte
+            // bias loads, which need N % 4 == 0; other N take the
+            // register-staged kernel below.)
+            if (act != MSST_ACT_NONE && N % 4 == 0)
                 return launch_f16_dma<128, 128, 32, 3, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act,
                                                                    s);
-            if (N % 256 == 128)
+            if (act == MSST_ACT_NONE && N % 256 == 128)
                 return launch_f16_dma<256, 128, 32, 3, 2, 2, OutT>(xh, wh, bias, res, o, m, n, k, act,
                                                                    s);
-            return launch_f16_dma<256, 256, 32, 3, 1, 4, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
+            if (act == MSST_ACT_NONE)
+                return launch_f16_dma<256, 256, 32, 3, 1, 4, OutT>(xh, wh, bias, res, o, m, n, k, act,
+                                                                   s);
         }
         const bool vec_ok = (K % 8 == 0) && aligned(x, 16) && aligned(w, 16);
         if (!vec_ok)
