@@ -9,13 +9,15 @@
 // MI355X layout decision: the reference transposes the fp32 activation
 // [B,T,F,dim] <-> [B,F,T,dim] twice per depth (permute().contiguous()).
 // Every op of a transformer except attention is token-wise, so this driver
-// transposes once on entry to the time-major order [B,F,T,dim], keeps it for
-// all 2*depth transformers, and lets the attention kernel address the
-// frequency-axis sequences with a token stride (msst_seq_layout):
-//   time layer : sequence (b,f), position t -> token (b*F + f)*T + t
-//   freq layer : sequence (b,t), position f -> token b*F*T + f*T + t
-// and transposes back once on exit.
-//
+// keeps x in place in the caller's order [B,T,F,dim] for all 2*depth
+// transformers and lets the attention kernel address either axis's
+// sequences with token strides (msst_seq_layout):
+//   time layer : sequence (b,f), position t -> token (b*T + t)*F + f
+//   freq layer : sequence (b,t), position f -> token (b*T + t)*F + f
+// (no transposes at all; an earlier version transposed once to [B,F,T,dim]
+// on entry and once back on exit, 2 x 31 us per BSRoformer chunk).
+// msst_roformer_transformer, the single-transformer entry, takes the
+// time-major order [B,F,T,dim].
 // Per transformer (fp16 weights):
 //   rms_norm_gate   x(f32) -> xn(f16), gates(f32)   [HBM]
 //   linear + RoPE   xn -> qkv(f16), q/k rotated      [MFMA]
@@ -42,7 +44,7 @@ constexpr int64_t kAlign = 256;
 int64_t round_up(int64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct StackBuffers {
-    int64_t xt, xn, big, merged, gates, tcos, tsin, fcos, fsin, total;
+    int64_t xn, big, merged, gates, tcos, tsin, fcos, fsin, total;
 };
 
 StackBuffers plan(const msst_stack_desc& d) {
@@ -52,7 +54,6 @@ StackBuffers plan(const msst_stack_desc& d) {
     const int64_t half = d.dim_head / 2;
     StackBuffers b{};
     int64_t off = 0;
-    b.xt = off; off += round_up(M * d.dim * 4);
     b.xn = off; off += round_up(M * d.dim * ab);
     const int64_t big = (3 * hd > d.ff_dim ? 3 * hd : d.ff_dim);
     b.big = off; off += round_up(M * big * ab);
@@ -107,8 +108,9 @@ int run_transformer(const msst_stack_desc& d, const msst_layer_weights& w, float
     if (rope_in_gemm(d, w)) {
         // fp16: RoPE rides in the QKV GEMM epilogue (q and k columns); the
         // attention kernel then reads pre-rotated q/k.  Position of token
-        // row r: (r / tok_pos) % seq_len for both axes of the time-major
-        // layout (time: t = r % T; frequency: f = (r / T) % F).
+        // row r: (r / tok_pos) % seq_len for both axes of either layout
+        // (stack, [B,T,F]: t = (r / F) % T, f = r % F; single transformer,
+        // [B,F,T]: t = r % T, f = (r / T) % F).
         MSST_TRY(msst_linear_rope(xn, w.w_qkv, nullptr, qkv, M, d.dim, 3 * hd, cos_t, sin_t,
                                   2 * hd, d.dim_head, L.tok_pos, L.seq_len, s));
         MSST_TRY(msst_gated_rope_attention(qkv, dt, 3 * hd, nullptr, nullptr, gates, merged, hd,
@@ -167,7 +169,6 @@ extern "C" int msst_roformer_stack(float* x, const msst_stack_desc* desc,
     }
     hipStream_t s = as_stream(stream);
     char* ws = reinterpret_cast<char*>(workspace);
-    float* xt = reinterpret_cast<float*>(ws + b.xt);
     float* tcos = reinterpret_cast<float*>(ws + b.tcos);
     float* tsin = reinterpret_cast<float*>(ws + b.tsin);
     float* fcos = reinterpret_cast<float*>(ws + b.fcos);
@@ -176,21 +177,19 @@ extern "C" int msst_roformer_stack(float* x, const msst_stack_desc* desc,
 
     MSST_TRY(msst_rope_table_device((int)T, (int)d.dim_head, tcos, tsin, s));
     MSST_TRY(msst_rope_table_device((int)F, (int)d.dim_head, fcos, fsin, s));
-    // [B,T,F,dim] -> [B,F,T,dim] once.
-    MSST_TRY(msst_swap_axes12(x, xt, MSST_F32, B, T, F, d.dim, s));
-
-    const msst_seq_layout time_l{B * F, 1, T, T, 0, 1};
-    const msst_seq_layout freq_l{B, T, F, F * T, 1, T};
+    // x is worked on in place in its own [B,T,F,dim] order:
+    //   time layer : sequence (b,f), position t -> token (b*T + t)*F + f
+    //   freq layer : sequence (b,t), position f -> token (b*T + t)*F + f
+    const msst_seq_layout time_l{B, F, T, T * F, 1, F};
+    const msst_seq_layout freq_l{B * T, 1, F, F, 0, 1};
     for (int64_t i = 0; i < d.depth; ++i) {
-        MSST_TRY(run_transformer(d, layers[2 * i], xt, ws, b, time_l, tcos, tsin, s));
-        MSST_TRY(run_transformer(d, layers[2 * i + 1], xt, ws, b, freq_l, fcos, fsin, s));
+        MSST_TRY(run_transformer(d, layers[2 * i], x, ws, b, time_l, tcos, tsin, s));
+        MSST_TRY(run_transformer(d, layers[2 * i + 1], x, ws, b, freq_l, fcos, fsin, s));
     }
     // BSRoformer final norm (model_bs_roformer.cu:538-539), token-wise.
     if (final_gamma)
-        MSST_TRY(msst_rms_norm(xt, MSST_F32, final_gamma, sqrtf((float)d.dim), xt, MSST_F32,
+        MSST_TRY(msst_rms_norm(x, MSST_F32, final_gamma, sqrtf((float)d.dim), x, MSST_F32,
                                B * T * F, d.dim, s));
-    // [B,F,T,dim] -> [B,T,F,dim] once.
-    MSST_TRY(msst_swap_axes12(xt, x, MSST_F32, B, F, T, d.dim, s));
     return MSST_OK;
 }
 
