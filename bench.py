@@ -250,14 +250,16 @@ def kernel_table(msst, torch, layers, B):
     tcos, tsin = msst.rope_table_device(FRAMES, DH)
     fcos, fsin = msst.rope_table_device(BANDS, DH)
     scale = math.sqrt(DIM)
-    time_l = msst.seq_layout(B * BANDS, 1, FRAMES, FRAMES, 0, 1)
-    freq_l = msst.seq_layout(B, FRAMES, BANDS, BANDS * FRAMES, 1, FRAMES)
+    # Token order [B, FRAMES, BANDS] as in the stack: time sequences are
+    # strided by BANDS tokens, frequency sequences contiguous.
+    time_l = msst.seq_layout(B, BANDS, FRAMES, FRAMES * BANDS, 1, BANDS)
+    freq_l = msst.seq_layout(B * FRAMES, 1, BANDS, BANDS, 0, 1)
     # (name, fn, flops, bytes) — bytes count each tensor read/written once.
     ents = [
         ("rms_norm_gate", lambda: msst.rms_norm_gate(x, w["attn_gamma"], scale, w["w_gate"],
                                                      w["b_gate"], out=xn, gates=gates),
          0, M * DIM * (4 + 2) + M * HEADS * 4),
-        ("gemm_qkv_rope", lambda: msst.linear_rope(xn, w["w_qkv"], tcos, tsin, 2 * hd, DH, 1,
+        ("gemm_qkv_rope", lambda: msst.linear_rope(xn, w["w_qkv"], tcos, tsin, 2 * hd, DH, BANDS,
                                                    FRAMES, out=qkv),
          2.0 * M * DIM * 3 * hd, 2 * M * DIM + 2 * 3 * hd * DIM + 2 * M * 3 * hd),
         ("attention_time", lambda: msst.gated_rope_attention(qkv, time_l, HEADS, None, None,
