@@ -214,28 +214,37 @@ def ff1_inputs(torch, layers, M):
     return xn, hid, layers[0]["w_ff1"], layers[0]["b_ff1"]
 
 
-def pmc_sample(msst, torch, B):
-    """Launch sequence for the counter passes: a plain copy kernel of known
-    size (256 MiB read + 256 MiB written, fp32 negation), then the FF1 GEMM;
-    three launches each, synchronised, nothing else timed."""
+def pmc_sample(msst, torch, B, which):
+    """Launch sequence for the counter passes, synchronised, nothing timed.
+
+    which == "ff1": a plain copy kernel of known size (256 MiB read + 256 MiB
+    written, fp32 negation), then the FF1 GEMM, three launches each (the
+    traffic calibration).  which == "kernels": the copy, then every kernel of
+    one transformer in stack order, three launches each (kernel_table's
+    launches; the counter tables split the dispatches in that order)."""
     layers, _ = make_weights(torch, 0, torch.float16)
     src = torch.randn(64 << 20, device="cuda")
     dst = torch.empty_like(src)
-    xn, hid, w1, b1 = ff1_inputs(torch, layers, B * FRAMES * BANDS)
+    if which == "ff1":
+        xn, hid, w1, b1 = ff1_inputs(torch, layers, B * FRAMES * BANDS)
+        ents = [("gemm_ff1_gelu", lambda: msst.linear(xn, w1, b1, "gelu", out=hid))]
+    else:
+        ents = [(name, fn) for name, fn, _, _ in kernel_ops(msst, torch, layers, B)]
     torch.cuda.synchronize()
     for _ in range(3):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
-    for _ in range(3):
-        msst.linear(xn, w1, b1, "gelu", out=hid)
-    torch.cuda.synchronize()
-    print(json.dumps({"pmc_sample": "copy 268435456 B read + 268435456 B written x3; "
-                                    "FF1 GEMM x3"}))
+    for _, fn in ents:
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+    print(json.dumps({"pmc_sample": "copy 268435456 B read + 268435456 B written x3; then x3 "
+                                    "each: " + ", ".join(n for n, _ in ents)}))
 
 
-def kernel_table(msst, torch, layers, B):
-    """Each kernel of one transformer alone, HIP-event timed on the stream it
-    runs on (50 launches after one warm-up)."""
+def kernel_ops(msst, torch, layers, B):
+    """Every kernel of one transformer as (name, launch, flops, bytes), on
+    seeded inputs of the stack's shapes."""
     M = B * FRAMES * BANDS
     hd = HEADS * DH
     w = layers[0]
@@ -278,6 +287,13 @@ def kernel_table(msst, torch, layers, B):
                                                   out=res),
          2.0 * M * FF * DIM, 2 * M * FF + 2 * DIM * FF + 8 * M * DIM),
     ]
+    return ents
+
+
+def kernel_table(msst, torch, layers, B):
+    """Each kernel of one transformer alone, HIP-event timed on the stream it
+    runs on (50 launches after one warm-up)."""
+    ents = kernel_ops(msst, torch, layers, B)
     table = {}
     for name, fn, flops, nbytes in ents:
         fn()
@@ -356,9 +372,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=1, help="chunks per step (config 5 uses 4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
-    ap.add_argument("--pmc-sample", action="store_true",
-                    help="run only the copy-kernel calibration and the FF1 GEMM (3 launches "
-                         "each), for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--pmc-sample", nargs="?", const="ff1", choices=("ff1", "kernels"),
+                    help="run only the copy-kernel calibration and then the FF1 GEMM (ff1) or "
+                         "every kernel of one transformer (kernels), 3 launches each, for "
+                         "rocprofv3 --pmc passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -372,7 +389,7 @@ def main():
     torch.manual_seed(0)
     B = args.batch
     if args.pmc_sample:
-        pmc_sample(msst, torch, B)
+        pmc_sample(msst, torch, B, args.pmc_sample)
         return
     layers, final_gamma = make_weights(torch, 0, torch.float16)
     st = msst.RoformerStack(layers, final_gamma, B, FRAMES, BANDS, DIM, HEADS, DH, FF, msst.F16)

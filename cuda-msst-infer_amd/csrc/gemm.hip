@@ -420,7 +420,8 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
     // One workgroup per CU only: at two per CU (the 256 x 128 tiles) the
     // stack measured slower with it (MelBandRoformer 6.14 -> 6.22 ms per
     // chunk), against 15.53 -> 15.44 for the 256 x 256 BSRoformer stack.
-    constexpr bool kResInAcc = EPI == kEpiRes && std::is_same<OutT, float>::value && MINB == 1;
+    constexpr bool kResInAcc = EPI == kEpiRes && ACT == MSST_ACT_NONE &&
+                               std::is_same<OutT, float>::value && MINB == 1;
     bool res_in_acc = false;
     if constexpr (kResInAcc) {
         res_in_acc = vec != 0 && n0 + wn * WN + WN <= N;
@@ -560,6 +561,230 @@ __global__ __launch_bounds__(128 * NWN, MINB) void gemm_f16_dma_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Ping-pong fp16 GEMM: 256 x 256 tiles, 8 waves in two groups of four (one
+// wave of each group per SIMD), LDS-DMA ring of NSTG k-tiles of BK.
+//
+// Group g owns rows 128 g .. 128 g + 127 of the tile; within a group wave
+// w % 4 owns 64 columns (a 128 x 64 wave tile of 4 x 2 32x32 blocks, as in
+// gemm_f16_dma_kernel).  The groups run half a k-tile apart: while one
+// group's waves issue the k-tile's MFMAs (at raised wave priority), the
+// other group's waves read their next k-tile's fragments from LDS and issue
+// their share of the ring's DMAs, so each SIMD's MFMA pipe is fed by one
+// wave or the other at every moment.  Every phase ends at a workgroup
+// barrier that both groups pass:
+//
+//   barrier:  B0    B1    B2    B3    B4   ...
+//   group 0:  | mem 0 | mma 0 | mem 1 | mma 1 | ...
+//   group 1:  |       | mem 0 | mma 0 | mem 1 | ...
+//
+// (group 1 passes one extra barrier before its loop).  The memory phase of
+// k-tile t also issues the DMA of k-tile t + NSTG - 1 into the slot of
+// t - 1, which both groups finished reading before barrier B(2t) (group 1
+// reads t - 1 between B(2t - 1) and B(2t)).  Right after its memory phase
+// of k-tile t (so before B(2t + 2), ahead of group 0's read of k-tile
+// t + 1), every wave waits until its own DMAs of k-tile t + 1 have landed:
+// each wave issues INST DMAs per k-tile, in k-tile order, and at that point
+// the newest ones it has issued belong to k-tiles t + 2 .. t + NSTG - 1, so
+// vmcnt((NSTG - 2) INST) leaves exactly those in flight.  Past the last
+// k-tile the DMAs re-fetch it into the free slot (every wait count stays
+// the same); the last wait of each wave is vmcnt(0), so no DMA is in flight
+// when the epilogue stages through the ring (group 0 after B(2 KT), group 1
+// after its last MFMAs; their staging regions are disjoint).
+// ---------------------------------------------------------------------------
+template <int BK, int NSTG, int EPI, int ACT, typename OutT>
+__global__ __launch_bounds__(512, 1) void gemm_pp_kernel(
+    const half_t* __restrict__ A, const half_t* __restrict__ W, const float* __restrict__ bias,
+    const OutT* residual, OutT* out, int M, int N, int K, int act, int tiles_n, int per_xcd,
+    int vec, EpiRope rope) {
+    constexpr int BM = 256, BN = 256, NW = 8;
+    constexpr int CPR = BK / 8;              // 16-byte chunks per LDS row
+    constexpr int RPD = 64 / CPR;            // rows per 1 KB DMA instruction
+    constexpr int KK = BK / 16;              // MFMA k-substeps per k-tile
+    constexpr int WM = 128, WN = 64;
+    constexpr int MI = WM / 32, NI = WN / 32;
+    constexpr int A_INST = BM / RPD / NW;    // DMA instructions per wave per k-tile
+    constexpr int B_INST = BN / RPD / NW;
+    constexpr int INST = A_INST + B_INST;
+    constexpr int STAGE = (BM + BN) * BK;
+    static_assert(A_INST * RPD * NW == BM && B_INST * RPD * NW == BN, "DMA split");
+    static_assert(NSTG >= 2 && (NSTG - 1) * INST <= 63, "vmcnt range");
+    __shared__ __attribute__((aligned(16))) half_t lds[NSTG][STAGE];
+
+    int tm, tn;
+    tile_coords(tiles_n, per_xcd, tm, tn, ((M + BM - 1) / BM) * tiles_n);
+    if (tm < 0) return;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    // Wave-uniform (readfirstlane: the group branch below is a scalar one).
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wid >> 2;
+    const int wm = grp, wn = wid & 3;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+
+    const int a_bytes = M * K * 2, b_bytes = N * K * 2;
+    const int sub_row = lane / CPR;
+    uint32_t aoff[A_INST], boff[B_INST];
+#pragma unroll
+    for (int i = 0; i < A_INST; ++i) {
+        const int rl = (wid * A_INST + i) * RPD + sub_row;
+        const int lchunk = (lane % CPR) ^ chunk_swz<BK>(rl);
+        aoff[i] = (uint32_t)(min(m0 + rl, M - 1) * K + lchunk * 8) * 2u;
+    }
+#pragma unroll
+    for (int i = 0; i < B_INST; ++i) {
+        const int rl = (wid * B_INST + i) * RPD + sub_row;
+        const int lchunk = (lane % CPR) ^ chunk_swz<BK>(rl);
+        boff[i] = (uint32_t)(min(n0 + rl, N - 1) * K + lchunk * 8) * 2u;
+    }
+    auto issue = [&](int k0, int slot) {  // this wave's INST DMAs of the k-tile at k0
+        const uint32_t kb = (uint32_t)k0 * 2u;
+#pragma unroll
+        for (int i = 0; i < A_INST; ++i)
+            dma16(A, a_bytes, lds[slot] + (wid * A_INST + i) * 512, aoff[i] + kb);
+#pragma unroll
+        for (int i = 0; i < B_INST; ++i)
+            dma16(W, b_bytes, lds[slot] + BM * BK + (wid * B_INST + i) * 512, boff[i] + kb);
+    };
+
+    f16x acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = f16x{};
+
+    // Accumulators that start from the fp32 residual (whole-width wave
+    // tiles) or from the bias (activation epilogues), read ahead of the
+    // ring's first DMAs as in gemm_f16_dma_kernel.
+    constexpr bool kResInAcc = EPI == kEpiRes && ACT == MSST_ACT_NONE &&
+                               std::is_same<OutT, float>::value;
+    constexpr bool kBiasInAcc = EPI == kEpiPlain && ACT != MSST_ACT_NONE;
+    bool res_in_acc = false;
+    if constexpr (kResInAcc) {
+        res_in_acc = vec != 0 && n0 + wn * WN + WN <= N;
+        const int wrow0 = __builtin_amdgcn_readfirstlane(m0 + wm * WM);
+        const int nrows = res_in_acc ? max(0, min(M - wrow0, WM)) : 0;
+        const float* rbase = uniform_ptr(reinterpret_cast<const float*>(residual) +
+                                         (int64_t)max(wrow0, 0) * N);
+        const int rbytes = __builtin_amdgcn_readfirstlane(nrows * N * 4);
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int c = n0 + wn * WN + j * 32 + 8 * g + 4 * lhalf;
+                    const f4 r = load16_bounded(rbase, rbytes, ((i * 32 + lrow) * N + c) * 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] = r[e];
+                }
+    }
+    if constexpr (kBiasInAcc) {
+        const float* bb = uniform_ptr(bias);
+        const int bbytes = bias ? N * 4 : 0;
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int c = n0 + wn * WN + j * 32 + 8 * g + 4 * lhalf;
+                const f4 b = load16_bounded(bb, bbytes, (uint32_t)c * 4u);
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * g + e] = b[e];
+            }
+    }
+
+    const int KT = K / BK;
+    // Prologue: k-tiles 0 .. NSTG-2 (clamped for short K: the last k-tile
+    // is re-fetched, which keeps the per-k-tile DMA count fixed).
+#pragma unroll
+    for (int st = 0; st < NSTG - 1; ++st) issue(min(st, KT - 1) * BK, st);
+    if constexpr (kResInAcc || kBiasInAcc) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NI; ++j) use_now(acc[i][j]);
+    }
+
+    h8 af[KK][MI], bf[KK][NI];
+    auto mem_phase = [&](int t) {
+        const int slot = t % NSTG;
+        const half_t* As = lds[slot];
+        const half_t* Bs = lds[slot] + BM * BK;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            const int c = kk * 2 + lhalf;
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int r = wm * WM + i * 32 + lrow;
+                af[kk][i] = *reinterpret_cast<const h8*>(As + r * BK + ((c ^ chunk_swz<BK>(r)) << 3));
+            }
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                const int r = wn * WN + j * 32 + lrow;
+                bf[kk][j] = *reinterpret_cast<const h8*>(Bs + r * BK + ((c ^ chunk_swz<BK>(r)) << 3));
+            }
+        }
+        const int tn2 = t + NSTG - 1;
+        issue(min(tn2, KT - 1) * BK, tn2 % NSTG);
+    };
+    auto mma_phase = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NI; ++j)
+                    acc[i][j] = mfma32x32x16(bf[kk][j], af[kk][i], acc[i][j]);
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Own DMAs of the next k-tile landed (the last wait drains the ring).
+    auto wait_next = [&](int t) {
+        if (t + 1 < KT)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTG - 2) * INST) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+
+    // Both groups run the same loop body (one copy of the code: separate
+    // loops per group made the register allocator shuffle and spill the
+    // accumulators); group 1 passes one barrier before it, group 0 one
+    // after it, so group 1 runs one phase behind.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NSTG - 2) * INST) : "memory");  // k-tile 0
+    if (grp == 1) lds_barrier();  // B(0)
+    for (int t = 0; t < KT; ++t) {
+        lds_barrier();  // group 0: B(2t), group 1: B(2t + 1)
+        mem_phase(t);
+        wait_next(t);
+        lds_barrier();  // group 0: B(2t + 1), group 1: B(2t + 2)
+        mma_phase();
+    }
+    if (grp == 0) lds_barrier();  // B(2 KT)
+
+    constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / NW);
+    constexpr bool kSwz = 32 * (WN + 4) > kRegion;
+    constexpr int kIP = pick_ip<MI, kSwz ? WN : WN + 4, kRegion>();
+    static_assert(kIP * 32 * (kSwz ? WN : WN + 4) <= kRegion, "epilogue staging does not fit in LDS");
+    float* region = reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion;
+    if constexpr (kResInAcc) {
+        if (res_in_acc) {
+            store_tile_lds<MI, NI, kIP, kEpiPlain, OutT, true, ACT, kSwz>(
+                acc, region, lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act, nullptr, out,
+                vec != 0, rope);
+            return;
+        }
+    }
+    store_tile_lds<MI, NI, kIP, EPI, OutT, true, ACT, kSwz, kBiasInAcc>(
+        acc, region, lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act, residual, out, vec != 0,
+        rope);
+}
+
+// ---------------------------------------------------------------------------
 // Skinny GEMM for N <= 16 (the H-wide gate projection): one wave per row,
 // each lane a contiguous K slice, butterfly sums over the wave.
 // ---------------------------------------------------------------------------
@@ -660,6 +885,38 @@ void launch_dma_epi(const half_t* x, const half_t* w, const float* bias, const O
     hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, NSTG, MINB, NWN, EPI, ACT, OutT>),
                        dim3(grid), dim3(128 * NWN), 0, s, x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd,
                        vec_flag(res, out, N), rope);
+}
+
+template <int BK, int NSTG, int EPI, int ACT, typename OutT>
+void launch_pp_epi(const half_t* x, const half_t* w, const float* bias, const OutT* res,
+                   OutT* out, int M, int N, int K, int act, hipStream_t s, const EpiRope& rope) {
+    const int tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+    int per_xcd;
+    const int grid = num_xcd_slots((int64_t)tiles_m * tiles_n, per_xcd);
+    hipLaunchKernelGGL((gemm_pp_kernel<BK, NSTG, EPI, ACT, OutT>), dim3(grid), dim3(512), 0, s, x,
+                       w, bias, res, out, M, N, K, act, tiles_n, per_xcd, vec_flag(res, out, N),
+                       rope);
+}
+
+template <int BK, int NSTG, typename OutT>
+int launch_pp(const half_t* x, const half_t* w, const float* bias, const OutT* res, OutT* out,
+              int M, int N, int K, int act, hipStream_t s, const EpiRope* rope = nullptr) {
+    if (rope) {
+        if constexpr (std::is_same<OutT, half_t>::value)
+            launch_pp_epi<BK, NSTG, kEpiRope, MSST_ACT_NONE, OutT>(x, w, bias, res, out, M, N, K,
+                                                                   act, s, *rope);
+        else
+            return set_error(MSST_ERR_UNSUPPORTED, "RoPE epilogue needs fp16 output");
+    } else if (act != MSST_ACT_NONE) {
+        return set_error(MSST_ERR_UNSUPPORTED, "ping-pong GEMM takes no activation");
+    } else if (res) {
+        launch_pp_epi<BK, NSTG, kEpiRes, MSST_ACT_NONE, OutT>(x, w, bias, res, out, M, N, K, act,
+                                                              s, EpiRope{});
+    } else {
+        launch_pp_epi<BK, NSTG, kEpiPlain, MSST_ACT_NONE, OutT>(x, w, bias, res, out, M, N, K, act,
+                                                                s, EpiRope{});
+    }
+    return check_launch("gemm_pp_kernel");
 }
 
 // The activation is a template parameter of the kernel (its epilogue is
@@ -775,13 +1032,18 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
             // activation the epilogue is VALU-heavy and 128 x 128 tiles at
             // three workgroups per CU hide it behind the others' main loops;
             // otherwise one 256 x 256 tile per CU (8 waves) moves the fewest
-            // L2 -> LDS bytes per flop.  N = 128 (mod 256) (MelBandRoformer's
+            // L2 -> LDS bytes per flop, run by the ping-pong kernel (6-8 %
+            // faster than gemm_f16_dma_kernel on the same tiles, with
+            // bit-identical results; fp16 residuals keep the latter, whose
+            // epilogue residual fits the register budget).  N = 128 (mod 256) (MelBandRoformer's
             // dim 384) takes 256 x 128 tiles at two workgroups per CU instead
             // of padding a quarter of the 256-wide tiles (out-proj / FF2
             // 9-10 % faster).
             // (The activation kernels start their accumulators from 16-byte
             // bias loads, which need N % 4 == 0; other N take the
             // register-staged kernel below.)
+            if (act == MSST_ACT_NONE && N % 256 == 0 && (!res || std::is_same<OutT, float>::value))
+                return launch_pp<32, 3, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
             if (act != MSST_ACT_NONE && N % 4 == 0)
                 return launch_f16_dma<128, 128, 32, 3, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act,
                                                                    s);
@@ -868,6 +1130,9 @@ extern "C" int msst_linear_rope(const void* x, const void* w, const float* bias,
     const half_t* xh = reinterpret_cast<const half_t*>(x);
     const half_t* wh = reinterpret_cast<const half_t*>(w);
     half_t* oh = reinterpret_cast<half_t*>(out);
+    if (N % 256 == 0)
+        return launch_pp<32, 3, half_t>(xh, wh, bias, nullptr, oh, (int)M, (int)N, (int)K,
+                                        MSST_ACT_NONE, as_stream(stream), &r);
     return launch_f16_dma<256, 256, 32, 3, 1, 4, half_t>(xh, wh, bias, nullptr, oh, (int)M,
                                                          (int)N, (int)K, MSST_ACT_NONE,
                                                          as_stream(stream), &r);
