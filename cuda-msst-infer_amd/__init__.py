@@ -114,7 +114,12 @@ _SIGS = {
     "msst_hann_window": ([_vp, _int, _vp], _int),
     "msst_roformer_transformer": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights),
                                    _int, _vp, _i64, _vp], _int),
+    "msst_roformer_stack_noalloc": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights),
+                                     _vp, _vp], _int),
 }
+
+# Bytes of the library's own device scratch behind msst_roformer_stack_noalloc.
+STACK_SCRATCH_BYTES = 64 << 20
 
 EXPORTED = tuple(_SIGS)
 
@@ -348,6 +353,14 @@ class RoformerStack:
                                         _ptr(self.final_gamma), _ptr(self.workspace),
                                         self.workspace.numel(), _stream()),
               "msst_roformer_stack")
+        return x
+
+    def call_noalloc(self, x):
+        """Like __call__, through msst_roformer_stack_noalloc: the library's
+        own device scratch instead of self.workspace."""
+        check(lib().msst_roformer_stack_noalloc(_ptr(x), ctypes.byref(self.desc), self._arr,
+                                                _ptr(self.final_gamma), _stream()),
+              "msst_roformer_stack_noalloc")
         return x
 
     def transformer(self, x, layer: int, axis: int):

@@ -32,6 +32,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <mutex>
 #include <string>
 
 #include "msst_common.hpp"
@@ -147,28 +148,12 @@ extern "C" int64_t msst_roformer_stack_workspace(const msst_stack_desc* desc) {
     return plan(*desc).total;
 }
 
-extern "C" int msst_roformer_stack(float* x, const msst_stack_desc* desc,
-                                   const msst_layer_weights* layers, const float* final_gamma,
-                                   void* workspace, int64_t workspace_bytes, void* stream) {
-    using namespace msst;
-    MSST_REQUIRE(x && desc && workspace, MSST_ERR_INVALID_ARG, "null pointer");
-    const msst_stack_desc& d = *desc;
-    MSST_REQUIRE(desc_ok(d), MSST_ERR_INVALID_ARG,
-                 "bad descriptor (dim_head must be 64, heads <= 16, sizes positive)");
-    MSST_REQUIRE(d.depth == 0 || layers, MSST_ERR_INVALID_ARG, "null layer weights");
-    MSST_REQUIRE(aligned(workspace, kAlign), MSST_ERR_ALIGNMENT, "workspace not 256-byte aligned");
-    const StackBuffers b = plan(d);
-    MSST_REQUIRE(workspace_bytes >= b.total, MSST_ERR_WORKSPACE,
-                 "workspace holds " + std::to_string(workspace_bytes) + " bytes, needs " +
-                     std::to_string(b.total));
-    for (int64_t i = 0; i < 2 * d.depth; ++i) {
-        const msst_layer_weights& w = layers[i];
-        MSST_REQUIRE(w.attn_gamma && w.w_qkv && w.w_gate && w.b_gate && w.w_out && w.ff_gamma &&
-                         w.w_ff1 && w.b_ff1 && w.w_ff2 && w.b_ff2,
-                     MSST_ERR_INVALID_ARG, "layer " + std::to_string(i) + " has a null weight");
-    }
-    hipStream_t s = as_stream(stream);
-    char* ws = reinterpret_cast<char*>(workspace);
+namespace msst {
+namespace {
+
+// The stack on a workspace already checked for size and alignment.
+int stack_run(float* x, const msst_stack_desc& d, const msst_layer_weights* layers,
+              const float* final_gamma, char* ws, const StackBuffers& b, hipStream_t s) {
     float* tcos = reinterpret_cast<float*>(ws + b.tcos);
     float* tsin = reinterpret_cast<float*>(ws + b.tsin);
     float* fcos = reinterpret_cast<float*>(ws + b.fcos);
@@ -191,6 +176,83 @@ extern "C" int msst_roformer_stack(float* x, const msst_stack_desc* desc,
         MSST_TRY(msst_rms_norm(x, MSST_F32, final_gamma, sqrtf((float)d.dim), x, MSST_F32,
                                B * T * F, d.dim, s));
     return MSST_OK;
+}
+
+int check_stack_args(float* x, const msst_stack_desc* desc, const msst_layer_weights* layers) {
+    MSST_REQUIRE(x && desc, MSST_ERR_INVALID_ARG, "null pointer");
+    const msst_stack_desc& d = *desc;
+    MSST_REQUIRE(desc_ok(d), MSST_ERR_INVALID_ARG,
+                 "bad descriptor (dim_head must be 64, heads <= 16, sizes positive)");
+    MSST_REQUIRE(d.depth == 0 || layers, MSST_ERR_INVALID_ARG, "null layer weights");
+    for (int64_t i = 0; i < 2 * d.depth; ++i) {
+        const msst_layer_weights& w = layers[i];
+        MSST_REQUIRE(w.attn_gamma && w.w_qkv && w.w_gate && w.b_gate && w.w_out && w.ff_gamma &&
+                         w.w_ff1 && w.b_ff1 && w.w_ff2 && w.b_ff2,
+                     MSST_ERR_INVALID_ARG, "layer " + std::to_string(i) + " has a null weight");
+    }
+    return MSST_OK;
+}
+
+// Scratch of msst_roformer_stack_noalloc: the library's own device memory,
+// one copy per GPU (each device that loads the code object holds it until
+// the process ends).  Host code never passes `scratch` itself to a kernel
+// or copy (on the host it only names the symbol); it uses the device
+// address hipGetSymbolAddress returns, looked up once per device with that
+// device current.
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) char scratch[MSST_STACK_SCRATCH_BYTES];
+std::mutex g_scratch_mu;
+char* g_scratch_addr[kMaxDevices];
+
+int scratch_for_current_device(char** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    MSST_REQUIRE(e == hipSuccess, MSST_ERR_LAUNCH, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    MSST_REQUIRE(dev >= 0 && dev < kMaxDevices, MSST_ERR_UNSUPPORTED, "device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        MSST_REQUIRE(e == hipSuccess && p, MSST_ERR_LAUNCH,
+                     std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        g_scratch_addr[dev] = reinterpret_cast<char*>(p);
+    }
+    *out = g_scratch_addr[dev];
+    return MSST_OK;
+}
+
+}  // namespace
+}  // namespace msst
+
+extern "C" int msst_roformer_stack(float* x, const msst_stack_desc* desc,
+                                   const msst_layer_weights* layers, const float* final_gamma,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+    using namespace msst;
+    MSST_TRY(check_stack_args(x, desc, layers));
+    MSST_REQUIRE(workspace, MSST_ERR_INVALID_ARG, "null workspace");
+    MSST_REQUIRE(aligned(workspace, kAlign), MSST_ERR_ALIGNMENT, "workspace not 256-byte aligned");
+    const StackBuffers b = plan(*desc);
+    MSST_REQUIRE(workspace_bytes >= b.total, MSST_ERR_WORKSPACE,
+                 "workspace holds " + std::to_string(workspace_bytes) + " bytes, needs " +
+                     std::to_string(b.total));
+    return stack_run(x, *desc, layers, final_gamma, reinterpret_cast<char*>(workspace), b,
+                     as_stream(stream));
+}
+
+extern "C" int msst_roformer_stack_noalloc(float* x, const msst_stack_desc* desc,
+                                           const msst_layer_weights* layers,
+                                           const float* final_gamma, void* stream) {
+    using namespace msst;
+    MSST_TRY(check_stack_args(x, desc, layers));
+    const StackBuffers b = plan(*desc);
+    MSST_REQUIRE(b.total <= MSST_STACK_SCRATCH_BYTES, MSST_ERR_WORKSPACE,
+                 "the stack needs " + std::to_string(b.total) +
+                     " bytes of workspace, more than the library's scratch of " +
+                     std::to_string((long long)MSST_STACK_SCRATCH_BYTES) +
+                     " bytes: use msst_roformer_stack with a caller workspace");
+    char* ws = nullptr;
+    MSST_TRY(scratch_for_current_device(&ws));
+    return stack_run(x, *desc, layers, final_gamma, ws, b, as_stream(stream));
 }
 
 extern "C" int msst_roformer_transformer(float* x, const msst_stack_desc* desc,

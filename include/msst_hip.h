@@ -247,6 +247,21 @@ int msst_roformer_stack(float* x, const msst_stack_desc* desc,
                         const float* final_gamma, void* workspace,
                         int64_t workspace_bytes, void* stream);
 
+/* msst_roformer_stack with no workspace argument and no allocation: the
+ * workspace is the library's own static device scratch of
+ * MSST_STACK_SCRATCH_BYTES per GPU.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc).
+ * Descriptors whose msst_roformer_stack_workspace(desc) exceeds the scratch
+ * (about 10 800 tokens of a dim-512 stack) fail with MSST_ERR_WORKSPACE.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap on
+ * one GPU (other streams, other host threads) race and must be serialised
+ * by the caller.  Nothing in the scratch needs to start at zero. */
+#define MSST_STACK_SCRATCH_BYTES (64LL << 20)
+int msst_roformer_stack_noalloc(float* x, const msst_stack_desc* desc,
+                                const msst_layer_weights* layers,
+                                const float* final_gamma, void* stream);
+
 /* One transformer (apply_transformer with depth 1, model_bs_roformer.cu:
  * 310-331 / model_mel_band_roformer.cu:621-651) in place on the fp32
  * activation x in time-major token order [batch, bands, frames, dim]:
