@@ -66,6 +66,7 @@ class BandConfig(ctypes.Structure):
 
 
 _BCP = ctypes.POINTER(BandConfig)
+_P64 = ctypes.POINTER(_i64)
 _PP = ctypes.POINTER(_vp)
 
 _SIGS = {
@@ -116,6 +117,9 @@ _SIGS = {
                                    _int, _vp, _i64, _vp], _int),
     "msst_roformer_stack_noalloc": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights),
                                      _vp, _vp], _int),
+    "msst_complex_mul": ([_vp, _vp, _vp, _i64, _vp], _int),
+    "msst_strided_copy": ([_vp, _P64, _vp, _P64, _P64, _int, _int, _vp], _int),
+    "msst_binary": ([_vp, _P64, _vp, _P64, _vp, _P64, _int, _int, _int, _vp], _int),
 }
 
 # Bytes of the library's own device scratch behind msst_roformer_stack_noalloc.

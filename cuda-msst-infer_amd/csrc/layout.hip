@@ -7,6 +7,8 @@
 //   msst_cast              f32 <-> f16 (tensor.cu:1269-1294)
 //   msst_add               elementwise add (tensor.cu:1365-1447)
 //   msst_tanh              elementwise tanh (ops_elementwise.cu:84-88, :138)
+//   msst_complex_mul       product of interleaved complex pairs
+//                          (ops_elementwise.cu:267-303)
 //   msst_glu               last-axis GLU, first half * sigmoid(second half)
 //                          (ops_elementwise.cu:321-388)
 //   msst_chunk_extract     one chunk of the chunked driver: the audio seen
@@ -97,6 +99,18 @@ __global__ __launch_bounds__(256) void tanh_kernel(const T* x, T* out, int64_t n
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (; i < n; i += stride) out[i] = (T)tanhf((float)x[i]);
+}
+
+// (a.re + i a.im)(b.re + i b.im) per interleaved complex pair.
+__global__ __launch_bounds__(256) void complex_mul_kernel(const float2* __restrict__ a,
+                                                          const float2* __restrict__ b,
+                                                          float2* out, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        const float2 x = a[i], y = b[i];
+        out[i] = make_float2(x.x * y.x - x.y * y.y, x.x * y.y + x.y * y.x);
+    }
 }
 
 // out[r, j] = x[r, j] * 1 / (1 + exp(-x[r, j + half])), x [rows, 2 half].
@@ -293,6 +307,20 @@ extern "C" int msst_add(const void* a, const void* b, void* out, int dtype, int6
                            reinterpret_cast<const float*>(a), reinterpret_cast<const float*>(b),
                            reinterpret_cast<float*>(out), n);
     return check_launch("add_kernel");
+}
+
+extern "C" int msst_complex_mul(const float* a, const float* b, float* out, int64_t n,
+                                void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(a && b && out, MSST_ERR_INVALID_ARG, "null tensor pointer");
+    MSST_REQUIRE(n >= 0, MSST_ERR_INVALID_ARG, "negative size");
+    MSST_REQUIRE(aligned(a, 8) && aligned(b, 8) && aligned(out, 8), MSST_ERR_ALIGNMENT,
+                 "complex pairs must be 8-byte aligned");
+    if (n == 0) return MSST_OK;
+    hipLaunchKernelGGL(complex_mul_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream),
+                       reinterpret_cast<const float2*>(a), reinterpret_cast<const float2*>(b),
+                       reinterpret_cast<float2*>(out), n);
+    return check_launch("complex_mul_kernel");
 }
 
 extern "C" int msst_tanh(const void* x, void* out, int dtype, int64_t n, void* stream) {

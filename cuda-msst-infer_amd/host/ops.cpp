@@ -40,8 +40,8 @@ void check(int rc, const char* what) {
 void* stream() { return CudaContext::instance().stream(); }
 
 // Biases, gammas and RoPE tables are consumed as fp32 (the reference's
-// ensure_f32 on them).
-Tensor f32(const Tensor& t) { return t.to_f32(); }
+// ensure_f32 on them), row-major.
+Tensor f32(const Tensor& t) { return t.contiguous().to_f32(); }
 
 std::vector<int64_t> with_last(const std::vector<int64_t>& s, int64_t last) {
     std::vector<int64_t> o = s;
@@ -50,8 +50,9 @@ std::vector<int64_t> with_last(const std::vector<int64_t>& s, int64_t last) {
 }
 
 // Shared GEMM driver: act(x . W^T + b) written as out_dtype.
-Tensor gemm(const char* name, const Tensor& x, const Tensor& w, const Tensor* bias, int act,
+Tensor gemm(const char* name, const Tensor& xv, const Tensor& wv, const Tensor* bias, int act,
             DType out_dtype) {
+    const Tensor x = xv.contiguous(), w = wv.contiguous();
     if (w.ndim() != 2) throw std::runtime_error(std::string(name) + ": weight must be 2-D [out, in]");
     if (x.ndim() < 1) throw std::runtime_error(std::string(name) + ": x must have a last dim");
     const int64_t N = w.size(0), K = w.size(1);
@@ -86,7 +87,8 @@ DType act_out(const Tensor& x) { return x.dtype() == DType::Float16 ? DType::Flo
 }  // namespace
 
 // ops_norm.cu:455-491
-Tensor rms_norm(const Tensor& x, const Tensor& gamma, float scale) {
+Tensor rms_norm(const Tensor& xv, const Tensor& gamma, float scale) {
+    const Tensor x = xv.contiguous();
     if (x.ndim() < 1) throw std::runtime_error("rms_norm: x must have a last dim");
     const int64_t D = x.size(-1);
     if (gamma.numel() != D)
@@ -185,7 +187,8 @@ Tensor mel_filterbank(int sr, int n_fft, int n_mels, float fmin, float fmax) {
 }
 
 // ops_elementwise.cu:84-88, :138
-Tensor tanh_act(const Tensor& x) {
+Tensor tanh_act(const Tensor& xv) {
+    const Tensor x = xv.contiguous();
     Tensor out = Tensor::empty(x.shape(), x.dtype());
     if (x.numel() > 0)
         check(msst_tanh(x.data_ptr(), out.data_ptr(), abi(x.dtype()), x.numel(), stream()),
@@ -193,8 +196,40 @@ Tensor tanh_act(const Tensor& x) {
     return out;
 }
 
+// ops_elementwise.cu:282-299: fp32 product of interleaved (re, im) pairs,
+// cast back to a's dtype.
+Tensor complex_mul(const Tensor& a, const Tensor& b) {
+    if (a.ndim() < 1 || a.size(-1) != 2)
+        throw std::runtime_error("complex_mul: last dimension must be 2 (re, im)");
+    if (a.shape() != b.shape())
+        throw std::runtime_error("complex_mul: shapes " + a.shape_str() + " and " + b.shape_str() +
+                                 " differ");
+    const Tensor af = f32(a), bf = f32(b);
+    Tensor out = Tensor::empty(a.shape(), DType::Float32);
+    if (a.numel() > 0)
+        check(msst_complex_mul(af.data_f32(), bf.data_f32(), out.data_f32(), a.numel() / 2,
+                               stream()),
+              "complex_mul");
+    return out.to_dtype(a.dtype());
+}
+
+// ops_elementwise.cu:503-527: a copy of x with index `index` along dim set
+// to value (the fill is a broadcast strided copy into that slice).
+Tensor index_fill(const Tensor& x, int dim, int64_t index, float value) {
+    const int n = x.ndim();
+    const int d = dim < 0 ? dim + n : dim;
+    if (d < 0 || d >= n) throw std::out_of_range("index_fill: dim out of range");
+    if (index < 0 || index >= x.size(d))
+        throw std::out_of_range("index_fill: index " + std::to_string(index) + " out of range");
+    Tensor out = x.clone();
+    Tensor sl = out.slice(d, index, index + 1);
+    sl.copy_from(Tensor::full({1}, value, x.dtype()).expand(sl.shape()));
+    return out;
+}
+
 // ops_elementwise.cu:345-388 (last dimension)
-Tensor glu(const Tensor& x, int dim) {
+Tensor glu(const Tensor& xv, int dim) {
+    const Tensor x = xv.contiguous();
     const int nd = x.ndim();
     if (nd < 1 || (dim != -1 && dim != nd - 1))
         throw std::runtime_error("glu: only the last dimension is supported");
@@ -248,9 +283,10 @@ Tensor scaled_dot_product_attention(const Tensor& q, const Tensor& k, const Tens
                                  ", k " + k.shape_str() + ", v " + v.shape_str() +
                                  " do not agree");
     // One element type for the kernel: k and v follow q.
-    Tensor kc = k.to_dtype(q.dtype()), vc = v.to_dtype(q.dtype());
+    const Tensor qc = q.contiguous();
+    const Tensor kc = k.contiguous().to_dtype(q.dtype()), vc = v.contiguous().to_dtype(q.dtype());
     Tensor out = Tensor::empty(q.shape(), q.dtype());
-    check(msst_attention(q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
+    check(msst_attention(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
                          abi(q.dtype()), B, H, N, Nk, D, scale, stream()),
           "scaled_dot_product_attention");
     return out;
@@ -267,16 +303,20 @@ void apply_rotary_emb(Tensor& q, Tensor& k, const Tensor& cos_freqs, const Tenso
     if (cos_freqs.numel() < N * (D / 2) || sin_freqs.numel() < N * (D / 2))
         throw std::runtime_error("apply_rotary_emb: cos/sin tables smaller than [N, D/2]");
     Tensor c = f32(cos_freqs), s = f32(sin_freqs);
-    check(msst_rope_qk(q.data_ptr(), k.data_ptr(), abi(q.dtype()), c.data_f32(), s.data_f32(), B,
+    // In place; views are rotated through row-major copies written back.
+    Tensor qc = q.contiguous(), kc = k.contiguous();
+    check(msst_rope_qk(qc.data_ptr(), kc.data_ptr(), abi(q.dtype()), c.data_f32(), s.data_f32(), B,
                        H, N, D, stream()),
           "apply_rotary_emb");
+    if (qc.data_ptr() != q.data_ptr()) q.copy_from(qc);
+    if (kc.data_ptr() != k.data_ptr()) k.copy_from(kc);
 }
 
 // model_bs_roformer.cu:482-539 / model_mel_band_roformer.cu:843-906
 void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int heads, int dim_head,
                     const Tensor& final_gamma) {
-    if (x.ndim() != 4 || x.dtype() != DType::Float32)
-        throw std::runtime_error("roformer_stack: x must be fp32 [B, T, F, dim]");
+    if (x.ndim() != 4 || x.dtype() != DType::Float32 || !x.is_contiguous())
+        throw std::runtime_error("roformer_stack: x must be a contiguous fp32 [B, T, F, dim]");
     if (layers.size() % 2 != 0)
         throw std::runtime_error("roformer_stack: layers must alternate time/frequency (even count)");
     msst_stack_desc d{};
@@ -433,7 +473,8 @@ void copy2d(void* dst, int64_t dst_pitch, const void* src, int64_t src_pitch, in
 }
 }  // namespace
 
-Tensor BandPlan::band_gather(const Tensor& stft, int64_t batch) const {
+Tensor BandPlan::band_gather(const Tensor& stftv, int64_t batch) const {
+    const Tensor stft = stftv.contiguous();
     if (stft_.channels == 0) throw std::runtime_error("band_gather: plan has no STFT side");
     if (stft.ndim() != 4 || stft.dtype() != DType::Float32 || stft.size(3) != 2 ||
         stft.size(0) != batch * stft_.channels || stft.size(1) != stft_.stft_bins)
@@ -449,8 +490,9 @@ Tensor BandPlan::band_gather(const Tensor& stft, int64_t batch) const {
     return out;
 }
 
-Tensor BandPlan::mask_merge(const Tensor& masks, const Tensor& stft, int64_t batch,
+Tensor BandPlan::mask_merge(const Tensor& masksv, const Tensor& stftv, int64_t batch,
                             bool zero_dc) const {
+    const Tensor masks = masksv.contiguous(), stft = stftv.contiguous();
     if (stft_.channels == 0) throw std::runtime_error("mask_merge: plan has no STFT side");
     int64_t ftot = 0;
     for (int d : dims_) ftot += d;
@@ -473,7 +515,8 @@ Tensor BandPlan::mask_merge(const Tensor& masks, const Tensor& stft, int64_t bat
     return out;
 }
 
-Tensor BandPlan::band_split(const Tensor& x) const {
+Tensor BandPlan::band_split(const Tensor& xv) const {
+    const Tensor x = xv.contiguous();
     int64_t ftot = 0;
     for (int d : dims_) ftot += d;
     if (x.ndim() < 1 || x.size(-1) != ftot || x.dtype() != DType::Float32)
@@ -508,7 +551,8 @@ Tensor BandPlan::band_split(const Tensor& x) const {
     return out;
 }
 
-Tensor BandPlan::mask_estimator(const Tensor& x) const {
+Tensor BandPlan::mask_estimator(const Tensor& xv) const {
+    const Tensor x = xv.contiguous();
     const int64_t nb = (int64_t)dims_.size();
     if (x.ndim() < 2 || x.size(-1) != dim_ || x.size(-2) != nb)
         throw std::runtime_error("mask_estimator: x must be [..., num_bands, dim]");

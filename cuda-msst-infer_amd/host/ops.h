@@ -97,6 +97,13 @@ Tensor mel_filterbank(int sr, int n_fft, int n_mels, float fmin = 0.0f, float fm
 Tensor tanh_act(const Tensor& x);
 Tensor glu(const Tensor& x, int dim = -1);
 
+// ops.h:51 and :121 (ops_elementwise.cu:267-303, :503-527): the mask side of
+// the Roformers' forward (the masked STFT, the zeroed DC bin).
+// complex_mul: [..., 2] interleaved (re, im), computed in fp32, returned in
+// a's dtype.  index_fill: a copy of x with slice `index` of dim set to value.
+Tensor complex_mul(const Tensor& a, const Tensor& b);
+Tensor index_fill(const Tensor& x, int dim, int64_t index, float value);
+
 Tensor linear_gelu(const Tensor& x, const Tensor& weight, const Tensor& bias);
 Tensor linear_silu(const Tensor& x, const Tensor& weight, const Tensor& bias);
 Tensor linear_sigmoid(const Tensor& x, const Tensor& weight, const Tensor& bias);

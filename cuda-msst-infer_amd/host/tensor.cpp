@@ -58,6 +58,30 @@ Tensor Tensor::zeros(std::vector<int64_t> shape, DType dtype) {
     return t;
 }
 
+Tensor Tensor::ones(std::vector<int64_t> shape, DType dtype) {
+    return full(std::move(shape), 1.0f, dtype);
+}
+
+// One element uploaded, then broadcast by a strided copy with zero source
+// strides.
+Tensor Tensor::full(std::vector<int64_t> shape, float value, DType dtype) {
+    Tensor t = empty(std::move(shape), dtype);
+    if (t.numel_ == 0) return t;
+    Tensor one = empty({1}, dtype);
+    if (dtype == DType::Float16) {
+        const __half h = __float2half(value);
+        one.copy_from_cpu(&h, sizeof h);
+    } else {
+        one.copy_from_cpu(&value, sizeof value);
+    }
+    const std::vector<int64_t> zero(t.shape_.size(), 0);
+    check_abi(msst_strided_copy(one.data_, zero.data(), t.data_, t.strides_.data(),
+                                t.shape_.data(), t.ndim(), (int)dtype_size(dtype),
+                                CudaContext::instance().stream()),
+              "Tensor::full");
+    return t;
+}
+
 Tensor Tensor::from_cpu_f32(const float* data, std::vector<int64_t> shape) {
     Tensor t = empty(std::move(shape), DType::Float32);
     t.copy_from_cpu(data, t.nbytes());
@@ -96,7 +120,19 @@ const __half* Tensor::data_f16() const {
     return static_cast<const __half*>(data_);
 }
 
+// tensor.cu:656-665: row-major strides, size-1 axes ignored.
+bool Tensor::is_contiguous() const {
+    if (numel_ <= 1) return true;
+    int64_t expected = 1;
+    for (int i = ndim() - 1; i >= 0; --i) {
+        if (shape_[i] != 1 && strides_[i] != expected) return false;
+        expected *= shape_[i];
+    }
+    return true;
+}
+
 void Tensor::copy_from_cpu(const void* src, size_t bytes) {
+    if (!is_contiguous()) throw std::runtime_error("Tensor::copy_from_cpu: not contiguous");
     if (bytes > nbytes()) throw std::runtime_error("Tensor::copy_from_cpu: too many bytes");
     if (bytes == 0) return;
     hipStream_t s = CudaContext::instance().stream();
@@ -105,6 +141,10 @@ void Tensor::copy_from_cpu(const void* src, size_t bytes) {
 }
 
 void Tensor::copy_to_cpu(void* dst, size_t bytes) const {
+    if (!is_contiguous()) {
+        contiguous().copy_to_cpu(dst, bytes);
+        return;
+    }
     if (bytes > nbytes()) throw std::runtime_error("Tensor::copy_to_cpu: too many bytes");
     if (bytes == 0) return;
     hipStream_t s = CudaContext::instance().stream();
@@ -139,7 +179,7 @@ Tensor Tensor::reshape(std::vector<int64_t> new_shape) const {
     if (known != numel_)
         throw std::runtime_error("Tensor::reshape: " + shape_str() + " has " +
                                  std::to_string(numel_) + " elements");
-    Tensor t = *this;
+    Tensor t = is_contiguous() ? *this : contiguous();
     t.shape_ = std::move(new_shape);
     t.compute_strides();
     return t;
@@ -158,14 +198,172 @@ Tensor Tensor::squeeze(int dim) const {
     const int n = ndim();
     const int d = dim < 0 ? dim + n : dim;
     if (d < 0 || d >= n) throw std::out_of_range("Tensor::squeeze: dim out of range");
-    if (shape_[d] != 1) return *this;
+    if (shape_[d] != 1)
+        throw std::runtime_error("Tensor::squeeze: dimension " + std::to_string(dim) + " of " +
+                                 shape_str() + " is not 1");
     std::vector<int64_t> s = shape_;
     s.erase(s.begin() + d);
     return reshape(s);
 }
 
+// tensor.cu:837-855: the same storage with reordered shape and strides.
+Tensor Tensor::permute(std::vector<int> dims) const {
+    const int n = ndim();
+    if ((int)dims.size() != n)
+        throw std::runtime_error("Tensor::permute: " + std::to_string(dims.size()) +
+                                 " dims for a " + std::to_string(n) + "-D tensor");
+    std::vector<bool> seen(n, false);
+    Tensor t = *this;
+    for (int i = 0; i < n; ++i) {
+        int d = dims[i] < 0 ? dims[i] + n : dims[i];
+        if (d < 0 || d >= n || seen[d])
+            throw std::runtime_error("Tensor::permute: dims are not a permutation");
+        seen[d] = true;
+        t.shape_[i] = shape_[d];
+        t.strides_[i] = strides_[d];
+    }
+    return t;
+}
+
+Tensor Tensor::transpose(int dim0, int dim1) const {
+    const int n = ndim();
+    const int a = dim0 < 0 ? dim0 + n : dim0, b = dim1 < 0 ? dim1 + n : dim1;
+    if (a < 0 || a >= n || b < 0 || b >= n)
+        throw std::out_of_range("Tensor::transpose: dim out of range");
+    std::vector<int> dims(n);
+    for (int i = 0; i < n; ++i) dims[i] = i;
+    std::swap(dims[a], dims[b]);
+    return permute(dims);
+}
+
+// tensor.cu:868-903: one strided-copy launch into a new row-major tensor.
+Tensor Tensor::contiguous() const {
+    if (is_contiguous()) return *this;
+    Tensor t = empty(shape_, dtype_);
+    t.copy_from(*this);
+    return t;
+}
+
+// tensor.cu:924-957: broadcast view, stride 0 along expanded axes (new
+// leading axes allowed).
+Tensor Tensor::expand(std::vector<int64_t> new_shape) const {
+    const int n = (int)new_shape.size(), k = ndim();
+    if (n < k) throw std::runtime_error("Tensor::expand: cannot drop dimensions");
+    Tensor t = *this;
+    t.shape_ = new_shape;
+    t.strides_.assign(n, 0);
+    t.numel_ = 1;
+    for (int i = 0; i < n; ++i) {
+        const int j = i - (n - k);  // aligned source axis
+        const int64_t src = j >= 0 ? shape_[j] : 1;
+        if (new_shape[i] == -1 && j >= 0) t.shape_[i] = src;
+        if (t.shape_[i] < 0) throw std::runtime_error("Tensor::expand: negative extent");
+        if (j >= 0 && src == t.shape_[i])
+            t.strides_[i] = strides_[j];
+        else if (src != 1)
+            throw std::runtime_error("Tensor::expand: " + shape_str() + " cannot expand to axis " +
+                                     std::to_string(i) + " of extent " +
+                                     std::to_string(t.shape_[i]));
+        t.numel_ *= t.shape_[i];
+    }
+    return t;
+}
+
+// tensor.cu:960-979: view of [start, end) along dim.
+Tensor Tensor::slice(int dim, int64_t start, int64_t end) const {
+    const int n = ndim();
+    const int d = dim < 0 ? dim + n : dim;
+    if (d < 0 || d >= n) throw std::out_of_range("Tensor::slice: dim out of range");
+    const int64_t ext = shape_[d];
+    if (start < 0) start += ext;
+    if (end < 0) end += ext;
+    start = std::max<int64_t>(start, 0);
+    end = std::min<int64_t>(end, ext);
+    if (start >= end) return Tensor();
+    Tensor t = *this;
+    t.shape_[d] = end - start;
+    t.numel_ = numel_ / ext * (end - start);
+    t.data_ = static_cast<char*>(data_) + start * strides_[d] * (int64_t)dtype_size(dtype_);
+    return t;
+}
+
+std::vector<Tensor> Tensor::split(int dim, const std::vector<int64_t>& sizes) const {
+    const int n = ndim();
+    const int d = dim < 0 ? dim + n : dim;
+    if (d < 0 || d >= n) throw std::out_of_range("Tensor::split: dim out of range");
+    int64_t total = 0;
+    for (int64_t s : sizes) total += s;
+    if (total != shape_[d])
+        throw std::runtime_error("Tensor::split: sizes sum to " + std::to_string(total) +
+                                 ", dimension has " + std::to_string(shape_[d]));
+    std::vector<Tensor> out;
+    int64_t off = 0;
+    for (int64_t s : sizes) {
+        out.push_back(slice(d, off, off + s));
+        off += s;
+    }
+    return out;
+}
+
+std::vector<Tensor> Tensor::unbind(int dim) const {
+    const int n = ndim();
+    const int d = dim < 0 ? dim + n : dim;
+    if (d < 0 || d >= n) throw std::out_of_range("Tensor::unbind: dim out of range");
+    std::vector<Tensor> out;
+    for (int64_t i = 0; i < shape_[d]; ++i) out.push_back(slice(d, i, i + 1).squeeze(d));
+    return out;
+}
+
+// tensor.cu:1062-1136: each input copied (strided, in place of the
+// reference's contiguous() + slab kernel) into its slab of the output.
+Tensor Tensor::cat(const std::vector<Tensor>& tensors, int dim) {
+    if (tensors.empty()) throw std::runtime_error("Tensor::cat: empty tensor list");
+    const Tensor& t0 = tensors[0];
+    const int n = t0.ndim();
+    const int d = dim < 0 ? dim + n : dim;
+    if (d < 0 || d >= n) throw std::out_of_range("Tensor::cat: dim out of range");
+    std::vector<int64_t> shape = t0.shape_;
+    int64_t total = 0;
+    for (const Tensor& t : tensors) {
+        if (t.ndim() != n) throw std::runtime_error("Tensor::cat: ndim mismatch");
+        if (t.dtype_ != t0.dtype_) throw std::runtime_error("Tensor::cat: dtype mismatch");
+        for (int i = 0; i < n; ++i)
+            if (i != d && t.shape_[i] != shape[i])
+                throw std::runtime_error("Tensor::cat: shape " + t.shape_str() + " vs " +
+                                         t0.shape_str());
+        total += t.shape_[d];
+    }
+    shape[d] = total;
+    Tensor out = empty(shape, t0.dtype_);
+    int64_t off = 0;
+    for (const Tensor& t : tensors) {
+        if (t.numel_ > 0) out.slice(d, off, off + t.shape_[d]).copy_from(t);
+        off += t.shape_[d];
+    }
+    return out;
+}
+
+// tensor.cu:1138-1150: unsqueeze every input at dim, then cat.
+Tensor Tensor::stack(const std::vector<Tensor>& tensors, int dim) {
+    if (tensors.empty()) throw std::runtime_error("Tensor::stack: empty tensor list");
+    const int n = tensors[0].ndim() + 1;
+    const int d = dim < 0 ? dim + n : dim;
+    std::vector<Tensor> u;
+    u.reserve(tensors.size());
+    for (const Tensor& t : tensors) {
+        // A view with a size-1 axis (no copy, unlike unsqueeze of a view).
+        if (d < 0 || d > t.ndim()) throw std::out_of_range("Tensor::stack: dim out of range");
+        Tensor v = t;
+        v.shape_.insert(v.shape_.begin() + d, 1);
+        v.strides_.insert(v.strides_.begin() + d, 0);
+        u.push_back(v);
+    }
+    return cat(u, d);
+}
+
 Tensor Tensor::to_dtype(DType new_dtype) const {
     if (new_dtype == dtype_) return *this;
+    if (!is_contiguous()) return contiguous().to_dtype(new_dtype);
     Tensor t = empty(shape_, new_dtype);
     if (numel_ > 0)
         check_abi(msst_cast(data_, abi_dtype(dtype_), t.data_, abi_dtype(new_dtype), numel_,
@@ -174,28 +372,94 @@ Tensor Tensor::to_dtype(DType new_dtype) const {
     return t;
 }
 
-Tensor Tensor::operator+(const Tensor& other) const {
-    if (other.dtype_ != dtype_) throw std::runtime_error("Tensor::operator+: dtype mismatch");
-    if (other.shape_ != shape_)
-        throw std::runtime_error("Tensor::operator+: shape " + shape_str() + " vs " +
-                                 other.shape_str());
-    Tensor t = empty(shape_, dtype_);
-    if (numel_ > 0)
+namespace {
+
+// Broadcast shape of a and b (trailing-axis alignment, size-1 axes), or
+// throws.
+std::vector<int64_t> broadcast_shape(const std::vector<int64_t>& a, const std::vector<int64_t>& b,
+                                     const char* what) {
+    const size_t n = std::max(a.size(), b.size());
+    std::vector<int64_t> out(n);
+    for (size_t i = 0; i < n; ++i) {
+        const int64_t x = i + a.size() >= n ? a[i + a.size() - n] : 1;
+        const int64_t y = i + b.size() >= n ? b[i + b.size() - n] : 1;
+        if (x != y && x != 1 && y != 1)
+            throw std::runtime_error(std::string(what) + ": shapes do not broadcast");
+        out[i] = x == 1 ? y : x;
+    }
+    return out;
+}
+
+// Element strides of t viewed at `shape` (t's axes aligned to the end;
+// stride 0 along broadcast axes).
+std::vector<int64_t> broadcast_strides(const Tensor& t, const std::vector<int64_t>& shape) {
+    const size_t n = shape.size(), k = (size_t)t.ndim();
+    std::vector<int64_t> s(n, 0);
+    for (size_t i = n - k; i < n; ++i) {
+        const size_t j = i - (n - k);
+        s[i] = t.shape()[j] == 1 ? 0 : t.strides()[j];
+    }
+    return s;
+}
+
+}  // namespace
+
+Tensor Tensor::binary(const Tensor& other, int op, const char* what) const {
+    if (other.dtype_ != dtype_) throw std::runtime_error(std::string(what) + ": dtype mismatch");
+    const std::vector<int64_t> shape = broadcast_shape(shape_, other.shape_, what);
+    if ((int)shape.size() > 8) throw std::runtime_error(std::string(what) + ": more than 8 dims");
+    Tensor t = empty(shape, dtype_);
+    if (t.numel_ == 0) return t;
+    if (op == MSST_BIN_ADD && shape_ == other.shape_ && is_contiguous() && other.is_contiguous()) {
         check_abi(msst_add(data_, other.data_, t.data_, abi_dtype(dtype_), numel_,
                            CudaContext::instance().stream()),
-                  "Tensor::operator+");
+                  what);
+        return t;
+    }
+    const std::vector<int64_t> sa = broadcast_strides(*this, shape);
+    const std::vector<int64_t> sb = broadcast_strides(other, shape);
+    check_abi(msst_binary(data_, sa.data(), other.data_, sb.data(), t.data_, shape.data(),
+                          (int)shape.size(), op, abi_dtype(dtype_), CudaContext::instance().stream()),
+              what);
     return t;
 }
 
-Tensor& Tensor::add_(const Tensor& other) {
-    if (other.dtype_ != dtype_) throw std::runtime_error("Tensor::add_: dtype mismatch");
-    if (other.shape_ != shape_)
-        throw std::runtime_error("Tensor::add_: shape " + shape_str() + " vs " +
-                                 other.shape_str());
-    if (numel_ > 0)
+void Tensor::binary_inplace(const Tensor& other, int op, const char* what) {
+    if (other.dtype_ != dtype_) throw std::runtime_error(std::string(what) + ": dtype mismatch");
+    if (broadcast_shape(shape_, other.shape_, what) != shape_)
+        throw std::runtime_error(std::string(what) + ": " + other.shape_str() +
+                                 " does not broadcast to " + shape_str());
+    if (numel_ == 0) return;
+    if (!is_contiguous()) {
+        // In place on a view: compute into a contiguous temporary, write back.
+        Tensor t = binary(other, op, what);
+        copy_from(t);
+        return;
+    }
+    if (op == MSST_BIN_ADD && shape_ == other.shape_ && other.is_contiguous()) {
         check_abi(msst_add(data_, other.data_, data_, abi_dtype(dtype_), numel_,
                            CudaContext::instance().stream()),
-                  "Tensor::add_");
+                  what);
+        return;
+    }
+    const std::vector<int64_t> sb = broadcast_strides(other, shape_);
+    check_abi(msst_binary(data_, strides_.data(), other.data_, sb.data(), data_, shape_.data(),
+                          ndim(), op, abi_dtype(dtype_), CudaContext::instance().stream()),
+              what);
+}
+
+Tensor Tensor::operator+(const Tensor& other) const { return binary(other, MSST_BIN_ADD, "Tensor::operator+"); }
+Tensor Tensor::operator-(const Tensor& other) const { return binary(other, MSST_BIN_SUB, "Tensor::operator-"); }
+Tensor Tensor::operator*(const Tensor& other) const { return binary(other, MSST_BIN_MUL, "Tensor::operator*"); }
+Tensor Tensor::operator/(const Tensor& other) const { return binary(other, MSST_BIN_DIV, "Tensor::operator/"); }
+
+Tensor& Tensor::add_(const Tensor& other) {
+    binary_inplace(other, MSST_BIN_ADD, "Tensor::add_");
+    return *this;
+}
+
+Tensor& Tensor::mul_(const Tensor& other) {
+    binary_inplace(other, MSST_BIN_MUL, "Tensor::mul_");
     return *this;
 }
 
@@ -208,9 +472,22 @@ Tensor Tensor::clone() const {
 void Tensor::copy_from(const Tensor& src) {
     if (src.numel_ != numel_ || src.dtype_ != dtype_)
         throw std::runtime_error("Tensor::copy_from: size or dtype mismatch");
-    if (numel_ > 0)
+    if (numel_ == 0) return;
+    if (is_contiguous() && src.is_contiguous()) {
         HIP_CHECK(hipMemcpyAsync(data_, src.data_, nbytes(), hipMemcpyDeviceToDevice,
                                  CudaContext::instance().stream()));
+        return;
+    }
+    // Strided on either side: same shape required (the element order of a
+    // view is its index order).
+    if (src.shape_ != shape_)
+        throw std::runtime_error("Tensor::copy_from: shape " + src.shape_str() + " vs " +
+                                 shape_str());
+    if (ndim() > 8) throw std::runtime_error("Tensor::copy_from: more than 8 dims");
+    check_abi(msst_strided_copy(src.data_, src.strides_.data(), data_, strides_.data(),
+                                shape_.data(), ndim(), (int)dtype_size(dtype_),
+                                CudaContext::instance().stream()),
+              "Tensor::copy_from");
 }
 
 std::string Tensor::shape_str() const {

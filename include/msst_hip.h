@@ -56,7 +56,12 @@
  *   msst_cast                   tensor.cu:1269-1294 (to_dtype)
  *   msst_add                    tensor.cu:1365-1447 (operator+, add_)
  *   msst_swap_axes12            tensor.cu:868-903 (permute + contiguous)
+ *   msst_strided_copy           tensor.cu:868-903 (contiguous of a strided view),
+ *                               :1062-1150 (cat, stack)
+ *   msst_binary                 tensor.cu:1365-1447 (broadcast operator+ - * /,
+ *                               add_, mul_)
  *   msst_tanh                   ops.h:36 tanh_act      (ops_elementwise.cu:84-88, :138)
+ *   msst_complex_mul            ops.h:51 complex_mul   (ops_elementwise.cu:267-303)
  *   msst_glu                    ops.h:116 glu(x, -1)   (ops_elementwise.cu:321-388)
  *   msst_roformer_stack         model_bs_roformer.cu:482-539,
  *                               model_mel_band_roformer.cu:843-906
@@ -197,6 +202,10 @@ int msst_cast(const void* src, int src_dtype, void* dst, int dst_dtype,
 int msst_add(const void* a, const void* b, void* out, int dtype, int64_t n,
              void* stream);
 
+/* out[i] = a[i] * b[i] for n interleaved fp32 complex pairs (re, im); out
+ * may alias a or b. */
+int msst_complex_mul(const float* a, const float* b, float* out, int64_t n, void* stream);
+
 /* out = tanh(x), elementwise (in place allowed). */
 int msst_tanh(const void* x, void* out, int dtype, int64_t n, void* stream);
 
@@ -208,6 +217,28 @@ int msst_glu(const void* x, void* out, int dtype, int64_t rows, int64_t half, vo
  * depth loop (model_bs_roformer.cu:491, :509).  src and dst must differ. */
 int msst_swap_axes12(const void* src, void* dst, int dtype, int64_t A,
                      int64_t P, int64_t Q, int64_t R, void* stream);
+
+/* Strided views of cudasep::Tensor made real (tensor.cu:868-903 contiguous,
+ * :1062-1150 cat / stack): dst[i] = src[i] for every index i of `shape`
+ * (ndim <= 8), each side addressed by its own element strides (non-negative;
+ * src strides may be 0 for broadcast axes, dst strides must not map two
+ * indices to one element).  elem_bytes 1, 2, 4 or 8. */
+int msst_strided_copy(const void* src, const int64_t* src_strides, void* dst,
+                      const int64_t* dst_strides, const int64_t* shape, int ndim,
+                      int elem_bytes, void* stream);
+
+/* out = a op b elementwise over `shape` (ndim <= 8), out contiguous, a and b
+ * addressed by element strides (0 along broadcast axes): Tensor operator+ -
+ * * / and add_ / mul_ with broadcasting (tensor.cu:1365-1447).  fp16 is
+ * computed in fp32 and rounded.  out may alias an operand that is
+ * contiguous over `shape`. */
+#define MSST_BIN_ADD 0
+#define MSST_BIN_SUB 1
+#define MSST_BIN_MUL 2
+#define MSST_BIN_DIV 3
+int msst_binary(const void* a, const int64_t* a_strides, const void* b,
+                const int64_t* b_strides, void* out, const int64_t* shape, int ndim,
+                int op, int dtype, void* stream);
 
 /* Weights of one transformer (attention + feed-forward), as the Roformer
  * models hold them (model_bs_roformer.h:78-98).  Matrices are [out,in] in

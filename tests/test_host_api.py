@@ -3,7 +3,12 @@
 CPU: the library exports the reference's op names with the reference's
 signatures (src/ops.h:56, :65-66, :83-85, :99-100, :128-135).
 GPU: tests/cpp/test_host_ops checks every op against the CPU oracle, the
-dtype rules and the error behaviour (see that file for the tolerances).
+dtype rules and the error behaviour (see that file for the tolerances);
+tests/cpp/test_tensor_views checks the Tensor view surface (permute, slice,
+split, expand, cat, stack, broadcast operators) and runs the reference's own
+per-op apply_attention / apply_feedforward / apply_transformer /
+compute_rotary_cos_sin sequence and depth-loop permutes (model_bs_roformer.cu:
+205-331, :482-534) on [62, 801, 512] against the oracle's transformer.
 """
 from __future__ import annotations
 
@@ -15,6 +20,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HOST_LIB = os.path.join(ROOT, "cuda-msst-infer_amd", "libcudasep_amd.so")
 TEST_BIN = os.path.join(ROOT, "tests", "cpp", "_build", "test_host_ops")
+VIEWS_BIN = os.path.join(ROOT, "tests", "cpp", "_build", "test_tensor_views")
 
 SIGNATURES = [
     "cudasep::ops::linear(cudasep::Tensor const&, cudasep::Tensor const&, cudasep::Tensor const&)",
@@ -37,6 +43,20 @@ SIGNATURES = [
     "cudasep::clear_attention_graph_cache()",
     "cudasep::CudaContext::instance()",
     "cudasep::Tensor::empty(std::vector<long, std::allocator<long> >, cudasep::DType)",
+    # the Tensor path subset the reference's Roformer code calls (tensor.h:75-105)
+    "cudasep::Tensor::permute(std::vector<int, std::allocator<int> >) const",
+    "cudasep::Tensor::transpose(int, int) const",
+    "cudasep::Tensor::contiguous() const",
+    "cudasep::Tensor::expand(std::vector<long, std::allocator<long> >) const",
+    "cudasep::Tensor::slice(int, long, long) const",
+    "cudasep::Tensor::split(int, std::vector<long, std::allocator<long> > const&) const",
+    "cudasep::Tensor::unbind(int) const",
+    "cudasep::Tensor::cat(std::vector<cudasep::Tensor, std::allocator<cudasep::Tensor> > const&, int)",
+    "cudasep::Tensor::stack(std::vector<cudasep::Tensor, std::allocator<cudasep::Tensor> > const&, int)",
+    "cudasep::Tensor::operator*(cudasep::Tensor const&) const",
+    "cudasep::Tensor::operator+(cudasep::Tensor const&) const",
+    "cudasep::Tensor::add_(cudasep::Tensor const&)",
+    "cudasep::Tensor::is_contiguous() const",
 ]
 
 
@@ -56,6 +76,17 @@ def test_host_ops_against_oracle(cuda):
     print("running", TEST_BIN, flush=True)
     r = subprocess.run([TEST_BIN], capture_output=True, text=True, timeout=300)
     print(r.stdout[-4000:])
+    print(r.stderr[-2000:])
+    assert r.returncode == 0
+    assert r.stdout.rstrip().splitlines()[-1].startswith("OK:")
+
+
+@pytest.mark.gpu
+def test_tensor_views_and_reference_per_op_sequence(cuda):
+    assert os.path.exists(VIEWS_BIN), "build tests/cpp first (make -C tests/cpp)"
+    print("running", VIEWS_BIN, flush=True)
+    r = subprocess.run([VIEWS_BIN], capture_output=True, text=True, timeout=600)
+    print(r.stdout[-6000:])
     print(r.stderr[-2000:])
     assert r.returncode == 0
     assert r.stdout.rstrip().splitlines()[-1].startswith("OK:")
