@@ -118,6 +118,8 @@ _SIGS = {
     "msst_roformer_stack_noalloc": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights),
                                      _vp, _vp], _int),
     "msst_complex_mul": ([_vp, _vp, _vp, _i64, _vp], _int),
+    "msst_roformer_stack_layer": ([_vp, ctypes.POINTER(StackDesc), ctypes.POINTER(LayerWeights),
+                                   _int, _vp, _i64, _vp], _int),
     "msst_strided_copy": ([_vp, _P64, _vp, _P64, _P64, _int, _int, _vp], _int),
     "msst_binary": ([_vp, _P64, _vp, _P64, _vp, _P64, _int, _int, _int, _vp], _int),
 }
@@ -365,6 +367,15 @@ class RoformerStack:
         check(lib().msst_roformer_stack_noalloc(_ptr(x), ctypes.byref(self.desc), self._arr,
                                                 _ptr(self.final_gamma), _stream()),
               "msst_roformer_stack_noalloc")
+        return x
+
+    def layer(self, x, layer: int, axis: int):
+        """One transformer in place on x [batch, frames, bands, dim] fp32 (the
+        stack's layout); axis 0 = time, 1 = frequency."""
+        check(lib().msst_roformer_stack_layer(
+            _ptr(x), ctypes.byref(self.desc), ctypes.byref(self._arr[layer]), axis,
+            _ptr(self.workspace), self.workspace.numel(), _stream()),
+            "msst_roformer_stack_layer")
         return x
 
     def transformer(self, x, layer: int, axis: int):

@@ -255,6 +255,35 @@ extern "C" int msst_roformer_stack_noalloc(float* x, const msst_stack_desc* desc
     return stack_run(x, *desc, layers, final_gamma, ws, b, as_stream(stream));
 }
 
+extern "C" int msst_roformer_stack_layer(float* x, const msst_stack_desc* desc,
+                                         const msst_layer_weights* w, int axis, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+    using namespace msst;
+    MSST_REQUIRE(x && desc && w && workspace, MSST_ERR_INVALID_ARG, "null pointer");
+    const msst_stack_desc& d = *desc;
+    MSST_REQUIRE(desc_ok(d), MSST_ERR_INVALID_ARG,
+                 "bad descriptor (dim_head must be 64, heads <= 16, sizes positive)");
+    MSST_REQUIRE(axis == 0 || axis == 1, MSST_ERR_INVALID_ARG, "axis must be 0 (time) or 1 (freq)");
+    MSST_REQUIRE(w->attn_gamma && w->w_qkv && w->w_gate && w->b_gate && w->w_out && w->ff_gamma &&
+                     w->w_ff1 && w->b_ff1 && w->w_ff2 && w->b_ff2,
+                 MSST_ERR_INVALID_ARG, "null weight");
+    MSST_REQUIRE(aligned(workspace, kAlign), MSST_ERR_ALIGNMENT, "workspace not 256-byte aligned");
+    const StackBuffers b = plan(d);
+    MSST_REQUIRE(workspace_bytes >= b.total, MSST_ERR_WORKSPACE,
+                 "workspace holds " + std::to_string(workspace_bytes) + " bytes, needs " +
+                     std::to_string(b.total));
+    hipStream_t s = as_stream(stream);
+    char* ws = reinterpret_cast<char*>(workspace);
+    const int64_t B = d.batch, T = d.frames, F = d.bands;
+    float* cs = reinterpret_cast<float*>(ws + (axis == 0 ? b.tcos : b.fcos));
+    float* sn = reinterpret_cast<float*>(ws + (axis == 0 ? b.tsin : b.fsin));
+    MSST_TRY(msst_rope_table_device((int)(axis == 0 ? T : F), (int)d.dim_head, cs, sn, s));
+    // The stack's own [B,T,F,dim] addressing (stack_run).
+    const msst_seq_layout time_l{B, F, T, T * F, 1, F};
+    const msst_seq_layout freq_l{B * T, 1, F, F, 0, 1};
+    return run_transformer(d, *w, x, ws, b, axis == 0 ? time_l : freq_l, cs, sn, s);
+}
+
 extern "C" int msst_roformer_transformer(float* x, const msst_stack_desc* desc,
                                          const msst_layer_weights* w, int axis, void* workspace,
                                          int64_t workspace_bytes, void* stream) {

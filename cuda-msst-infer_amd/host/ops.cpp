@@ -315,10 +315,24 @@ void apply_rotary_emb(Tensor& q, Tensor& k, const Tensor& cos_freqs, const Tenso
 // model_bs_roformer.cu:482-539 / model_mel_band_roformer.cu:843-906
 void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int heads, int dim_head,
                     const Tensor& final_gamma) {
+    roformer_stack(x, layers, heads, dim_head, final_gamma, StackSchedule{});
+}
+
+// model_bs_roformer.cu:477-539 with time/freq_transformer_depth and
+// skip_connection: the fused msst_roformer_stack for the plain schedule,
+// else one msst_roformer_stack_layer per transformer layer.  The skip sums
+// x += store[0] + ... + store[d-1] run as x += S with S the running sum of
+// the stored depth outputs (one extra activation instead of depth of them;
+// the same terms, summed in another order).
+void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int heads, int dim_head,
+                    const Tensor& final_gamma, const StackSchedule& sched) {
     if (x.ndim() != 4 || x.dtype() != DType::Float32 || !x.is_contiguous())
         throw std::runtime_error("roformer_stack: x must be a contiguous fp32 [B, T, F, dim]");
-    if (layers.size() % 2 != 0)
-        throw std::runtime_error("roformer_stack: layers must alternate time/frequency (even count)");
+    const int td = sched.time_depth, fd = sched.freq_depth;
+    if (td < 1 || fd < 1) throw std::runtime_error("roformer_stack: transformer depths must be >= 1");
+    if (layers.size() % (size_t)(td + fd) != 0)
+        throw std::runtime_error("roformer_stack: layers must hold depth * (time_depth + "
+                                 "freq_depth) transformer layers");
     msst_stack_desc d{};
     d.batch = x.size(0);
     d.frames = x.size(1);
@@ -326,7 +340,8 @@ void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int hea
     d.dim = x.size(3);
     d.heads = heads;
     d.dim_head = dim_head;
-    d.depth = (int64_t)layers.size() / 2;
+    const int64_t depth = (int64_t)layers.size() / (td + fd);
+    d.depth = depth;
     d.ff_dim = layers.empty() ? 4 * d.dim : layers[0].w_ff1.size(0);
     const DType wdt = layers.empty() ? DType::Float32 : layers[0].w_qkv.dtype();
     d.w_dtype = abi(wdt);
@@ -342,8 +357,9 @@ void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int hea
     for (size_t i = 0; i < layers.size(); ++i) {
         const RoformerLayer& L = layers[i];
         for (const Tensor* m : {&L.w_qkv, &L.w_gate, &L.w_out, &L.w_ff1, &L.w_ff2})
-            if (m->dtype() != wdt)
-                throw std::runtime_error("roformer_stack: weight matrices must share one dtype");
+            if (m->dtype() != wdt || !m->is_contiguous())
+                throw std::runtime_error(
+                    "roformer_stack: weight matrices must be contiguous and share one dtype");
         lw[i].attn_gamma = vec(L.attn_gamma);
         lw[i].w_qkv = L.w_qkv.data_ptr();
         lw[i].w_gate = L.w_gate.data_ptr();
@@ -360,8 +376,31 @@ void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int hea
     const int64_t ws = msst_roformer_stack_workspace(&d);
     if (ws < 0) throw std::runtime_error(std::string("roformer_stack: ") + msst_last_error());
     Tensor work = Tensor::empty({ws}, DType::Float16);  // byte buffer (>= ws bytes)
-    check(msst_roformer_stack(x.data_f32(), &d, lw.data(), fg, work.data_ptr(), 2 * ws, stream()),
-          "roformer_stack");
+    if (td == 1 && fd == 1 && !sched.skip_connection) {
+        check(msst_roformer_stack(x.data_f32(), &d, lw.data(), fg, work.data_ptr(), 2 * ws,
+                                  stream()),
+              "roformer_stack");
+        return;
+    }
+    Tensor skip_sum;  // sum of the depth outputs stored so far
+    size_t li = 0;
+    for (int64_t dd = 0; dd < depth; ++dd) {
+        if (sched.skip_connection && dd > 0) x.add_(skip_sum);
+        for (int t = 0; t < td + fd; ++t, ++li)
+            check(msst_roformer_stack_layer(x.data_f32(), &d, &lw[li], t < td ? 0 : 1,
+                                            work.data_ptr(), 2 * ws, stream()),
+                  "roformer_stack");
+        if (sched.skip_connection && dd + 1 < depth) {
+            if (dd == 0)
+                skip_sum = x.clone();
+            else
+                skip_sum.add_(x);
+        }
+    }
+    if (fg)
+        check(msst_rms_norm(x.data_f32(), MSST_F32, fg, std::sqrt((float)d.dim), x.data_f32(),
+                            MSST_F32, x.numel() / d.dim, d.dim, stream()),
+              "roformer_stack");
 }
 
 // ---------------------------------------------------------------------------

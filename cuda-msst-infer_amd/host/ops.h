@@ -128,6 +128,21 @@ struct RoformerLayer {
 void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int heads,
                     int dim_head, const Tensor& final_gamma);
 
+// The depth loop's other configurations (model_bs_roformer.cu:477-487,
+// :531-535, the apply_transformer loop :319): each depth runs time_depth
+// time-axis layers then freq_depth frequency-axis layers (layers holds
+// depth * (time_depth + freq_depth) entries in that order, the
+// MelBandRoformer norm on the last layer of each transformer), and with
+// skip_connection x += sum of the previous depths' outputs before every
+// depth after the first.
+struct StackSchedule {
+    int time_depth = 1;
+    int freq_depth = 1;
+    bool skip_connection = false;
+};
+void roformer_stack(Tensor& x, const std::vector<RoformerLayer>& layers, int heads,
+                    int dim_head, const Tensor& final_gamma, const StackSchedule& schedule);
+
 // ---- Band split and mask estimator (model_bs_roformer.cu:337-414,
 // model_mel_band_roformer.cu:658-738) as grouped launches over all bands.
 // band_dims[b] = 2 * freqs_in_band * audio_channels (the reference's

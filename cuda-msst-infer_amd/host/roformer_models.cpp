@@ -82,8 +82,12 @@ MelBands compute_mel_bands(int sr, int n_fft, int num_bands, int channels) {
     return mb;
 }
 
-void RoformerModel::load_common(const ModelWeights& weights, int depth, int linears,
+void RoformerModel::load_common(const ModelWeights& weights, int depth, int time_depth,
+                                int freq_depth, bool skip_connection, int linears,
                                 bool transformer_norms) {
+    if (depth < 1 || time_depth < 1 || freq_depth < 1)
+        throw std::runtime_error("Roformer: depth and transformer depths must be >= 1");
+    schedule_ = ops::StackSchedule{time_depth, freq_depth, skip_connection};
     const int nb = (int)band_dims_.size();
     window_ = ops::hann_window(win_length_);
     // band_split.to_features.{b}.{0.gamma, 1.weight, 1.bias}
@@ -94,27 +98,29 @@ void RoformerModel::load_common(const ModelWeights& weights, int depth, int line
         split_w_.w.push_back(weights.get(p + ".1.weight"));
         split_w_.b.push_back(weights.get(p + ".1.bias"));
     }
-    // layers.{d}.{0 time, 1 freq}.layers.0.{0 attention, 1 feed-forward}
-    // (+ layers.{d}.{t}.norm.gamma closing each MelBandRoformer transformer)
+    // layers.{d}.{0 time, 1 freq}.layers.{i}.{0 attention, 1 feed-forward},
+    // i < the transformer's depth (+ layers.{d}.{t}.norm.gamma closing each
+    // MelBandRoformer transformer, after its last layer)
     layers_.clear();
     for (int d = 0; d < depth; ++d)
-        for (int t = 0; t < 2; ++t) {
-            const std::string tp = "layers." + std::to_string(d) + "." + std::to_string(t);
-            const std::string p = tp + ".layers.0";
-            ops::RoformerLayer L;
-            L.attn_gamma = weights.get(p + ".0.norm.gamma");
-            L.w_qkv = weights.get(p + ".0.to_qkv.weight");
-            L.w_gate = weights.get(p + ".0.to_gates.weight");
-            L.b_gate = weights.get(p + ".0.to_gates.bias");
-            L.w_out = weights.get(p + ".0.to_out.0.weight");
-            L.ff_gamma = weights.get(p + ".1.net.0.gamma");
-            L.w_ff1 = weights.get(p + ".1.net.1.weight");
-            L.b_ff1 = weights.get(p + ".1.net.1.bias");
-            L.w_ff2 = weights.get(p + ".1.net.4.weight");
-            L.b_ff2 = weights.get(p + ".1.net.4.bias");
-            if (transformer_norms) L.final_gamma = weights.get(tp + ".norm.gamma");
-            layers_.push_back(L);
-        }
+        for (int t = 0; t < 2; ++t)
+            for (int i = 0, n = t == 0 ? time_depth : freq_depth; i < n; ++i) {
+                const std::string tp = "layers." + std::to_string(d) + "." + std::to_string(t);
+                const std::string p = tp + ".layers." + std::to_string(i);
+                ops::RoformerLayer L;
+                L.attn_gamma = weights.get(p + ".0.norm.gamma");
+                L.w_qkv = weights.get(p + ".0.to_qkv.weight");
+                L.w_gate = weights.get(p + ".0.to_gates.weight");
+                L.b_gate = weights.get(p + ".0.to_gates.bias");
+                L.w_out = weights.get(p + ".0.to_out.0.weight");
+                L.ff_gamma = weights.get(p + ".1.net.0.gamma");
+                L.w_ff1 = weights.get(p + ".1.net.1.weight");
+                L.b_ff1 = weights.get(p + ".1.net.1.bias");
+                L.w_ff2 = weights.get(p + ".1.net.4.weight");
+                L.b_ff2 = weights.get(p + ".1.net.4.bias");
+                if (transformer_norms && i == n - 1) L.final_gamma = weights.get(tp + ".norm.gamma");
+                layers_.push_back(L);
+            }
     // mask_estimators.{s}.to_freqs.{b}.0.{2 i}.{weight, bias}, i < linears
     mask_w_.assign(stems_, ops::MaskEstimatorWeights{});
     for (int s = 0; s < stems_; ++s)
@@ -157,14 +163,12 @@ void BSRoformer::load(const ModelWeights& weights) {
     const int bins = std::accumulate(cfg_.freqs_per_bands.begin(), cfg_.freqs_per_bands.end(), 0);
     if (bins != n_fft_ / 2 + 1)
         throw std::runtime_error("BSRoformer: freqs_per_bands must cover n_fft / 2 + 1 bins");
-    if (cfg_.time_transformer_depth != 1 || cfg_.freq_transformer_depth != 1 || cfg_.skip_connection)
-        throw std::runtime_error(
-            "BSRoformer: only time/freq_transformer_depth 1 without skip connections is built");
     if (win_length_ != n_fft_) throw std::runtime_error("BSRoformer: stft_win_length must equal stft_n_fft");
     band_dims_.clear();
     for (int f : cfg_.freqs_per_bands) band_dims_.push_back(2 * f * channels_);
     freq_indices_.clear();
-    load_common(weights, cfg_.depth, cfg_.mask_estimator_depth, false);
+    load_common(weights, cfg_.depth, cfg_.time_transformer_depth, cfg_.freq_transformer_depth,
+                cfg_.skip_connection, cfg_.mask_estimator_depth, false);
     final_norm_gamma_ = weights.get("final_norm.gamma");
 }
 
@@ -182,9 +186,6 @@ void MelBandRoformer::load(const ModelWeights& weights) {
     dim_ = cfg_.dim;
     heads_ = cfg_.heads;
     dim_head_ = cfg_.dim_head;
-    if (cfg_.time_transformer_depth != 1 || cfg_.freq_transformer_depth != 1 || cfg_.skip_connection)
-        throw std::runtime_error(
-            "MelBandRoformer: only time/freq_transformer_depth 1 without skip connections is built");
     if (win_length_ != n_fft_)
         throw std::runtime_error("MelBandRoformer: stft_win_length must equal stft_n_fft");
     const int nb = cfg_.num_bands;
@@ -224,7 +225,8 @@ void MelBandRoformer::load(const ModelWeights& weights) {
     }
     band_dims_.clear();
     for (int cnt : counts) band_dims_.push_back(2 * cnt * channels_);
-    load_common(weights, cfg_.depth, cfg_.mask_estimator_depth + 1, true);
+    load_common(weights, cfg_.depth, cfg_.time_transformer_depth, cfg_.freq_transformer_depth,
+                cfg_.skip_connection, cfg_.mask_estimator_depth + 1, true);
     final_norm_gamma_ = Tensor();
 }
 
@@ -241,7 +243,7 @@ Tensor RoformerModel::forward(const Tensor& audio) {
                             normalized_);
     const int64_t T = spec.size(2);
     Tensor feats = plans_[0]->band_split(plans_[0]->band_gather(spec, B));  // [B, T, nb, dim]
-    ops::roformer_stack(feats, layers_, heads_, dim_head_, final_norm_gamma_);
+    ops::roformer_stack(feats, layers_, heads_, dim_head_, final_norm_gamma_, schedule_);
     int64_t ftot = 0;
     for (int d : band_dims_) ftot += d;
     Tensor masks = Tensor::empty({(int64_t)stems_, B, T, ftot});

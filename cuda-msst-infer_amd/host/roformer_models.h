@@ -106,7 +106,8 @@ protected:
     std::vector<int> band_dims_;        // 2 * bins * channels per band
     std::vector<int> freq_indices_;     // empty: every bin once, in order
     Tensor window_;
-    std::vector<ops::RoformerLayer> layers_;
+    std::vector<ops::RoformerLayer> layers_;  // per depth: time_depth, then freq_depth layers
+    ops::StackSchedule schedule_;
     Tensor final_norm_gamma_;           // BSRoformer only
     ops::BandSplitWeights split_w_;
     std::vector<ops::MaskEstimatorWeights> mask_w_;
@@ -114,7 +115,8 @@ protected:
 
     // Shared loading steps (the two models use the same weight names for
     // these parts).
-    void load_common(const ModelWeights& w, int depth, int linears, bool transformer_norms);
+    void load_common(const ModelWeights& w, int depth, int time_depth, int freq_depth,
+                     bool skip_connection, int linears, bool transformer_norms);
 };
 
 class BSRoformer : public RoformerModel {

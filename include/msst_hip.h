@@ -65,6 +65,8 @@
  *   msst_glu                    ops.h:116 glu(x, -1)   (ops_elementwise.cu:321-388)
  *   msst_roformer_stack         model_bs_roformer.cu:482-539,
  *                               model_mel_band_roformer.cu:843-906
+ *   msst_roformer_stack_layer   model_bs_roformer.cu:310-331 in the stack's
+ *                               layout (transformer depth > 1, skip sums :477-487)
  *   msst_roformer_transformer   model_bs_roformer.cu:310-331,
  *                               model_mel_band_roformer.cu:621-651
  */
@@ -277,6 +279,18 @@ int msst_roformer_stack(float* x, const msst_stack_desc* desc,
                         const msst_layer_weights* layers,
                         const float* final_gamma, void* workspace,
                         int64_t workspace_bytes, void* stream);
+
+/* One transformer (attention + feed-forward, and the MelBandRoformer
+ * output norm when w->final_gamma is set) in place on the stack's fp32
+ * activation x [batch, frames, bands, dim]: axis 0 attends over frames,
+ * axis 1 over bands.  For the depth loops msst_roformer_stack does not
+ * cover: time/freq_transformer_depth > 1 and skip connections
+ * (model_bs_roformer.cu:310-331, :477-487, :531-535).  Same workspace as
+ * msst_roformer_stack. */
+int msst_roformer_stack_layer(float* x, const msst_stack_desc* desc,
+                              const msst_layer_weights* w, int axis,
+                              void* workspace, int64_t workspace_bytes,
+                              void* stream);
 
 /* msst_roformer_stack with no workspace argument and no allocation: the
  * workspace is the library's own static device scratch of

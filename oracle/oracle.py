@@ -222,6 +222,45 @@ def roformer_stack(x, layers, heads: int, dim_head: int, final_gamma=None) -> np
     return x
 
 
+def roformer_stack_schedule(x, layers, heads: int, dim_head: int, final_gamma=None,
+                            time_depth: int = 1, freq_depth: int = 1,
+                            skip_connection: bool = False) -> np.ndarray:
+    """The depth loop of model_bs_roformer.cu:477-539 with its configuration
+    switches: per depth, skip_connection adds every stored earlier depth
+    output, one at a time (:482-487); then the time transformer on
+    [B*F, T, dim] (:488-505) as time_depth layers in sequence (the
+    apply_transformer loop, :319-327), the frequency transformer on
+    [B*T, F, dim] as freq_depth layers (:507-530); the depth output is stored
+    (:531-535).  layers: per depth, time_depth then freq_depth entries (a
+    MelBandRoformer transformer's closing norm on its last layer).
+    final_gamma: BSRoformer's final norm (:538-539)."""
+    x = _f32(x).copy()
+    B, T, F, dim = x.shape
+    per = time_depth + freq_depth
+    assert len(layers) % per == 0
+    depth = len(layers) // per
+    tc, ts = rope_table(T, dim_head)
+    fc, fs = rope_table(F, dim_head)
+    store = []
+    for d in range(depth):
+        if skip_connection:
+            for j in range(d):
+                x = x + store[j]
+        xt = np.ascontiguousarray(x.transpose(0, 2, 1, 3)).reshape(B * F, T, dim)
+        for i in range(time_depth):
+            xt = transformer(xt, layers[d * per + i], tc, ts, heads, dim_head)
+        x = np.ascontiguousarray(xt.reshape(B, F, T, dim).transpose(0, 2, 1, 3))
+        xf = x.reshape(B * T, F, dim)
+        for i in range(freq_depth):
+            xf = transformer(xf, layers[d * per + time_depth + i], fc, fs, heads, dim_head)
+        x = xf.reshape(B, T, F, dim)
+        if skip_connection:
+            store.append(x.copy())
+    if final_gamma is not None:
+        x = rms_norm(x, final_gamma, float(np.sqrt(dim)))
+    return x
+
+
 def glu(x) -> np.ndarray:
     """x [..., 2n] -> x[..., :n] * sigmoid(x[..., n:])."""
     x = _f32(x)
@@ -372,17 +411,26 @@ def _roformer_forward(cfg: dict, w: dict, audio, dims, fidx, depth: int, L: int,
         [w[f"band_split.to_features.{b}.1.bias"] for b in range(nb)])
     T = spec.shape[2]
     feats = feats.reshape(B, T, nb, -1)
+    td, fd = cfg.get("time_transformer_depth", 1), cfg.get("freq_transformer_depth", 1)
+    skip = bool(cfg.get("skip_connection", False))
     layers = []
     for d in range(depth):
-        for t in range(2):
-            p = f"layers.{d}.{t}.layers.0"
-            layers.append(LayerWeights(
-                w[p + ".0.norm.gamma"], w[p + ".0.to_qkv.weight"], w[p + ".0.to_gates.weight"],
-                w[p + ".0.to_gates.bias"], w[p + ".0.to_out.0.weight"], w[p + ".1.net.0.gamma"],
-                w[p + ".1.net.1.weight"], w[p + ".1.net.1.bias"], w[p + ".1.net.4.weight"],
-                w[p + ".1.net.4.bias"], w[f"layers.{d}.{t}.norm.gamma"] if per_norm else None))
-    feats = roformer_stack(feats, layers, cfg.get("heads", 8), cfg.get("dim_head", 64),
-                           final_gamma)
+        for t, n in ((0, td), (1, fd)):
+            for i in range(n):
+                p = f"layers.{d}.{t}.layers.{i}"
+                last = per_norm and i == n - 1
+                layers.append(LayerWeights(
+                    w[p + ".0.norm.gamma"], w[p + ".0.to_qkv.weight"],
+                    w[p + ".0.to_gates.weight"], w[p + ".0.to_gates.bias"],
+                    w[p + ".0.to_out.0.weight"], w[p + ".1.net.0.gamma"],
+                    w[p + ".1.net.1.weight"], w[p + ".1.net.1.bias"], w[p + ".1.net.4.weight"],
+                    w[p + ".1.net.4.bias"], w[f"layers.{d}.{t}.norm.gamma"] if last else None))
+    if td == 1 and fd == 1 and not skip:
+        feats = roformer_stack(feats, layers, cfg.get("heads", 8), cfg.get("dim_head", 64),
+                               final_gamma)
+    else:
+        feats = roformer_stack_schedule(feats, layers, cfg.get("heads", 8),
+                                        cfg.get("dim_head", 64), final_gamma, td, fd, skip)
     masks = []
     for s in range(stems):
         ws = [[w[f"mask_estimators.{s}.to_freqs.{b}.0.{2 * i}.weight"] for i in range(L)]

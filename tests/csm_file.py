@@ -55,9 +55,10 @@ def _roformer_weights(cfg: dict, band_bins, seed: int, unit_mask: bool, L: int,
         w[p + ".0.gamma"] = vec(d, m=1.0)
         w[p + ".1.weight"] = lin(dim, d)
         w[p + ".1.bias"] = vec(dim)
+    td, fd = cfg.get("time_transformer_depth", 1), cfg.get("freq_transformer_depth", 1)
     for d_ in range(depth):
-        for t in range(2):
-            p = f"layers.{d_}.{t}.layers.0"
+        for t, li in [(0, i) for i in range(td)] + [(1, i) for i in range(fd)]:
+            p = f"layers.{d_}.{t}.layers.{li}"
             w[p + ".0.norm.gamma"] = vec(dim, m=1.0)
             w[p + ".0.to_qkv.weight"] = lin(3 * inner, dim)
             w[p + ".0.to_gates.weight"] = lin(heads, dim)
@@ -68,7 +69,7 @@ def _roformer_weights(cfg: dict, band_bins, seed: int, unit_mask: bool, L: int,
             w[p + ".1.net.1.bias"] = vec(ff)
             w[p + ".1.net.4.weight"] = lin(dim, ff) * 0.5
             w[p + ".1.net.4.bias"] = vec(dim)
-            if per_norm:
+            if per_norm and li == (td if t == 0 else fd) - 1:
                 w[f"layers.{d_}.{t}.norm.gamma"] = vec(dim, 0.1, m=1.0)
     if final_norm:
         w["final_norm.gamma"] = vec(dim, m=1.0)

@@ -219,3 +219,29 @@ def test_cli_list_stems_and_errors(tmp_path, cuda):
     r = subprocess.run([CLI, "--model", str(model), "--input", str(wav), "--output", str(target),
                         "--stem", "1"], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and target.exists() and "sample rate" in r.stderr
+
+
+@pytest.mark.parametrize("model", ["bsr", "mbr"])
+@pytest.mark.parametrize("mode", ["fp32", "fp16"])
+def test_cli_skip_connection_and_transformer_depth(tmp_path, oracle, cuda, model, mode):
+    """Checkpoints with skip_connection and time/freq_transformer_depth 2
+    (model_bs_roformer.cu:477-487, :531-535, the apply_transformer loop
+    :319): depth 3, so the skip sums of two and three stored outputs run,
+    against the oracle's restatement of that loop."""
+    extra = {"depth": 3, "skip_connection": True, "time_transformer_depth": 2,
+             "freq_transformer_depth": 2}
+    rng = np.random.default_rng(77)
+    audio = (0.3 * rng.standard_normal((2, 3000))).astype(np.float32)
+    if model == "bsr":
+        cfg = dict(CFG, **extra)
+        w = csm_file.bsr_checkpoint(cfg, seed=8)
+    else:
+        cfg = dict(MBR_CFG, **extra)
+        w = mbr_model(oracle, cfg, seed=9)
+    print(f"skip/transformer-depth model {model} {mode}", flush=True)
+    y = separate(tmp_path, cfg, w, audio, mode)
+    r = oracle_separate(oracle, cfg, _fp16_view(w, mode), audio)
+    assert y.shape == r.shape
+    tol = 1e-4 if mode == "fp32" else TOL_F16
+    for s in range(y.shape[0]):
+        assert rel_err(y[s], r[s]) < tol, (s, rel_err(y[s], r[s]))

@@ -2,9 +2,10 @@
 oracle, at the BASELINE configurations.
 
   config 1  MelBandRoformer time layer, fp32, x [60, 801, 384]      (full size)
-  config 3  MelBandRoformer stack, fp16, dim 384, [60 bands, 801]   (depth 1 at
-            full size vs the oracle; depth 6 through the property tests)
-  config 4  BSRoformer stack, fp16, dim 512, [62 bands, 801]        (same)
+  config 3  MelBandRoformer stack, fp16, dim 384, [60 bands, 801]   (depth 1 and
+            the full depth 6 at full size vs the oracle; properties)
+  config 4  BSRoformer stack, fp16, dim 512, [62 bands, 801]        (depth 1 and
+            the full depth 12 at full size vs the oracle; properties)
   config 5  BSRoformer, batch of 4 chunks                           (batch
             consistency: bit-identical to 4 single-chunk runs)
 Weights: matrices and biases ~ N(0, 0.02), gammas 1 + N(0, 0.02), x ~ N(0,1).
@@ -101,6 +102,55 @@ def test_full_size_depth1_fp16(msst, oracle, cuda, name, F, dim, ff, mbr):
     """Configs 3/4 at full spatial size, one depth (time + freq layer)."""
     e = run_stack(msst, oracle, 1, 801, F, dim, 8, ff, 1, True, mbr, seed=4)
     assert e < TOL_F16, e
+
+
+@pytest.mark.parametrize("name,F,dim,ff,depth,mbr", [("bsr", 62, 512, 2048, 12, False),
+                                                     ("mbr", 60, 384, 1536, 6, True)])
+def test_full_depth_against_oracle(msst, oracle, cuda, name, F, dim, ff, depth, mbr):
+    """Configs 4 and 3 at full size and full depth against the oracle: the
+    12-depth BSRoformer stack with its final norm on [1, 801, 62, 512], the
+    6-depth MelBandRoformer stack with a norm closing every transformer on
+    [1, 801, 60, 384]; fp16 weights, fp32 residual."""
+    print(f"full-depth {name}: depth {depth}, [1, 801, {F}, {dim}]", flush=True)
+    e = run_stack(msst, oracle, 1, 801, F, dim, 8, ff, depth, True, mbr, seed=7)
+    print(f"full-depth {name}: max rel err {e:.3e}", flush=True)
+    assert e < TOL_F16, e
+
+
+@pytest.mark.parametrize("fp16", [False, True])
+@pytest.mark.parametrize("mbr", [False, True])
+def test_stack_layer_schedule_against_oracle(msst, oracle, cuda, fp16, mbr):
+    """msst_roformer_stack_layer driven through the depth loop's switches:
+    time/freq_transformer_depth 2 and skip_connection (the skip sums as
+    torch adds between calls), against the oracle's restatement of
+    model_bs_roformer.cu:477-539."""
+    B, T, F, dim, heads, ff, depth, td, fd = 1, 40, 9, 128, 2, 256, 3, 2, 2
+    per = td + fd
+    rng = np.random.default_rng(31)
+    layers = [R.random_layer(rng, dim, heads, 64, ff, final_norm=mbr and (i % per in (td - 1, per - 1)))
+              for i in range(depth * per)]
+    if fp16:
+        for w in layers:
+            for m in MATS:
+                w[m] = w[m].astype(np.float16).astype(np.float32)
+    fg = None if mbr else (1 + rng.standard_normal(dim) * 0.02).astype(np.float32)
+    x = rng.standard_normal((B, T, F, dim)).astype(np.float32)
+    st = build_stack(msst, layers, fp16, B, T, F, dim, heads, ff)
+    xd = torch.from_numpy(x).cuda()
+    stored = []
+    for d in range(depth):
+        for j in range(d):
+            xd += stored[j]
+        for i in range(per):
+            st.layer(xd, d * per + i, 0 if i < td else 1)
+        stored.append(xd.clone())
+    if fg is not None:
+        xd = msst.rms_norm(xd, torch.from_numpy(fg).cuda(), float(np.sqrt(dim)))
+    torch.cuda.synchronize()
+    r = oracle.roformer_stack_schedule(x, [oracle.LayerWeights(**w) for w in layers], heads, 64,
+                                       fg, td, fd, True)
+    e = rel_err(xd.cpu().numpy(), r)
+    assert e < (TOL_F16 if fp16 else TOL_F32), e
 
 
 @pytest.mark.parametrize("name,F,dim,ff,depth,mbr", [("bsr", 62, 512, 2048, 12, False),

@@ -673,3 +673,213 @@ def test_process_chunked_crossfade_closed_form(oracle):
         w = r(t)
         want = 500.0 / (1 + w)
         assert abs(y[t] - want) <= 1e-3 * want, (t, y[t], want)
+
+
+# ------------------------------------- depth-loop switches and forward chain
+def _identity_layer(rng, dim, H, Dh, ff, final_norm=False):
+    """A transformer whose attention and feed-forward branches are exactly 0
+    (zero out-projection, zero second linear and bias): x -> x, then the
+    optional closing norm."""
+    w = R.random_layer(rng, dim, H, Dh, ff, final_norm=final_norm)
+    w["w_out"][:] = 0.0
+    w["w_ff2"][:] = 0.0
+    w["b_ff2"][:] = 0.0
+    return w
+
+
+def test_stack_schedule_default_equals_stack(oracle):
+    """time/freq depth 1 without skip: the schedule restatement and the C
+    stack (pinned above against the torch composition) agree bit for bit."""
+    rng = np.random.default_rng(21)
+    B, T, Fb, dim, H, Dh, ff, depth = 2, 7, 5, 32, 2, 16, 64, 2
+    layers = [oracle.LayerWeights(**R.random_layer(rng, dim, H, Dh, ff, final_norm=(i % 2 == 1)))
+              for i in range(2 * depth)]
+    fg = (1 + rng.standard_normal(dim) * 0.02).astype(np.float32)
+    x = rng.standard_normal((B, T, Fb, dim)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.roformer_stack_schedule(x, layers, H, Dh, fg),
+                                  oracle.roformer_stack(x, layers, H, Dh, fg))
+
+
+def test_stack_schedule_skip_connection_closed_form(oracle):
+    """Identity transformers with skip_connection: depth d's output is
+    y_d = y_(d-1) + sum_(j<d) y_j (model_bs_roformer.cu:482-487 adds every
+    stored output, the previous depth's included), so y = x * (1, 2, 5, 13,
+    34)[depth - 1].  Values k/16 keep every sum exact in float32.  Storing
+    before the adds, or adding only the last output, gives other factors."""
+    rng = np.random.default_rng(22)
+    B, T, Fb, dim, H, Dh, ff = 1, 5, 3, 32, 2, 16, 64
+    x = (rng.integers(-100, 100, (B, T, Fb, dim)) / 16.0).astype(np.float32)
+    for depth, factor in ((1, 1), (2, 2), (3, 5), (4, 13), (5, 34)):
+        layers = [oracle.LayerWeights(**_identity_layer(rng, dim, H, Dh, ff))
+                  for _ in range(2 * depth)]
+        y = oracle.roformer_stack_schedule(x, layers, H, Dh, None, 1, 1, True)
+        np.testing.assert_array_equal(y, factor * x)
+        np.testing.assert_array_equal(
+            oracle.roformer_stack_schedule(x, layers, H, Dh, None, 1, 1, False), x)
+
+
+@pytest.mark.parametrize("mbr", [False, True])
+def test_stack_schedule_transformer_depth(oracle, mbr):
+    """time/freq_transformer_depth 2 whose second layers are identities equal
+    the depth-1 stack of the first layers (the closing MelBandRoformer norm on
+    the last layer of each transformer): a loop that runs the layers in
+    another order, interleaves the axes or applies the closing norm after
+    every layer fails it (RMSNorm with gamma != 1 is not idempotent)."""
+    rng = np.random.default_rng(23)
+    B, T, Fb, dim, H, Dh, ff, depth = 1, 6, 4, 32, 2, 16, 64, 2
+    firsts = [R.random_layer(rng, dim, H, Dh, ff) for _ in range(2 * depth)]
+    fgs = [(1 + rng.standard_normal(dim) * 0.3).astype(np.float32) for _ in range(2 * depth)]
+    sched, plain = [], []
+    for d in range(depth):
+        for t in range(2):
+            i = 2 * d + t
+            a = dict(firsts[i])
+            ident = _identity_layer(rng, dim, H, Dh, ff)
+            if mbr:
+                ident["final_gamma"] = fgs[i]
+                plain.append(oracle.LayerWeights(**dict(a, final_gamma=fgs[i])))
+            else:
+                plain.append(oracle.LayerWeights(**a))
+            sched += [oracle.LayerWeights(**a), oracle.LayerWeights(**ident)]
+    # per depth: time_depth (2) time layers, then freq_depth (2) freq layers
+    order = []
+    for d in range(depth):
+        order += [sched[4 * d], sched[4 * d + 1], sched[4 * d + 2], sched[4 * d + 3]]
+    x = rng.standard_normal((B, T, Fb, dim)).astype(np.float32)
+    y = oracle.roformer_stack_schedule(x, order, H, Dh, None, 2, 2, False)
+    r = oracle.roformer_stack(x, plain, H, Dh, None)
+    assert rel_err(y, r) < 1e-6
+    # the list order is per depth time layers then frequency layers: the
+    # interleaved order (time, freq, time, freq) runs the frequency weights
+    # on the time axis and must give another result
+    inter = []
+    for d in range(depth):
+        inter += [sched[4 * d], sched[4 * d + 2], sched[4 * d + 1], sched[4 * d + 3]]
+    assert rel_err(oracle.roformer_stack_schedule(x, inter, H, Dh, None, 2, 2, False), r) > 1e-3
+
+
+def _np_istft(spec, n_fft, hop, w, length):
+    """torch.istft restated with numpy: irfft per frame (the imaginary DC /
+    Nyquist parts drop out), window, overlap-add, divide by the summed
+    squared window where it exceeds 1e-8, trim the centre padding."""
+    X = spec[..., 0].astype(np.float64) + 1j * spec[..., 1]          # [B, F, T]
+    fr = np.fft.irfft(X.transpose(0, 2, 1), n=n_fft, axis=-1) * w    # [B, T, n_fft]
+    B, T = fr.shape[:2]
+    n = n_fft + hop * (T - 1)
+    out = np.zeros((B, n))
+    ws = np.zeros(n)
+    for t in range(T):
+        out[:, t * hop:t * hop + n_fft] += fr[:, t]
+        ws[t * hop:t * hop + n_fft] += w ** 2
+    out = np.where(ws > 1e-8, out / np.where(ws > 1e-8, ws, 1.0), out)
+    out = out[:, n_fft // 2:n - n_fft // 2]
+    return out if length < 0 else out[:, :length]
+
+
+def _np_rms(x, gamma, scale):
+    x = x.astype(np.float64)
+    return x / np.sqrt((x * x).sum(-1, keepdims=True) + 1e-12) * gamma * scale
+
+
+def _np_identity_forward(cfg, w, audio, dims, fidx, norms, L):
+    """float64 numpy chain of a Roformer forward whose transformers are
+    identities (model_bs_roformer.cu:420-609, model_mel_band_roformer.cu:
+    745-1040): STFT, 'b s f t c -> b t (f s) c' and the band bin selection
+    fidx (None: every bin in order), per band RMSNorm * sqrt(band width) +
+    linear, the RMSNorms `norms` in sequence (what is left of the stack: the
+    closing norms, or the final norm), per stem band MLPs of L linears (tanh
+    between) and GLU, complex masks averaged over the bands that hold each
+    bin, times the STFT, zero DC, stereo split, iSTFT."""
+    B, ch, S = audio.shape
+    n_fft, hop = cfg["stft_n_fft"], cfg["stft_hop_length"]
+    win = np.hanning(n_fft + 1)[:-1]
+    spec = _np_stft(audio.reshape(B * ch, S), n_fft, hop, win, True, False)   # [B*ch, F, T, 2]
+    F, T = spec.shape[1], spec.shape[2]
+    g = spec.reshape(B, ch, F, T, 2).transpose(0, 3, 2, 1, 4).reshape(B, T, F * ch, 2)
+    fi = np.arange(F * ch) if fidx is None else np.asarray(fidx)
+    x = g[:, :, fi].reshape(B, T, -1)
+    off = np.concatenate([[0], np.cumsum(dims)])
+    feats = []
+    for b, d in enumerate(dims):
+        p = f"band_split.to_features.{b}"
+        xb = _np_rms(x[..., off[b]:off[b + 1]], w[p + ".0.gamma"], math.sqrt(d))
+        feats.append(xb @ w[p + ".1.weight"].T.astype(np.float64) + w[p + ".1.bias"])
+    f = np.stack(feats, 2)                                                    # [B, T, nb, dim]
+    for gam in norms:
+        f = _np_rms(f, gam, math.sqrt(cfg["dim"]))
+    cnt = np.bincount(fi, minlength=F * ch).astype(np.float64)
+    outs = []
+    for s in range(cfg["num_stems"]):
+        mk = []
+        for b, d in enumerate(dims):
+            h = f[:, :, b]
+            for i in range(L):
+                p = f"mask_estimators.{s}.to_freqs.{b}.0.{2 * i}"
+                h = h @ w[p + ".weight"].T.astype(np.float64) + w[p + ".bias"]
+                if i < L - 1:
+                    h = np.tanh(h)
+            mk.append(h[..., :d] / (1.0 + np.exp(-h[..., d:])))
+        m = np.concatenate(mk, -1)
+        mc = m[..., 0::2] + 1j * m[..., 1::2]                                  # [B, T, n]
+        acc = np.zeros((B, T, F * ch), np.complex128)
+        np.add.at(acc, (slice(None), slice(None), fi), mc)
+        mean = (acc / np.maximum(cnt, 1e-8)).reshape(B, T, F, ch)
+        xc = (spec[..., 0] + 1j * spec[..., 1]).reshape(B, ch, F, T)
+        o = xc * mean.transpose(0, 3, 2, 1)                                    # [B, ch, F, T]
+        if cfg.get("zero_dc", True):
+            o[:, :, 0] = 0
+        o = np.stack([o.real, o.imag], -1).reshape(B * ch, F, T, 2)
+        outs.append(_np_istft(o, n_fft, hop, win, -1).reshape(B, ch, -1))
+    return np.stack(outs, 1)                                                   # [B, stems, ch, S']
+
+
+def _zero_branches(w, depth):
+    for d in range(depth):
+        for t in range(2):
+            p = f"layers.{d}.{t}.layers.0"
+            w[p + ".0.to_out.0.weight"][:] = 0.0
+            w[p + ".1.net.4.weight"][:] = 0.0
+            w[p + ".1.net.4.bias"][:] = 0.0
+
+
+def test_bsroformer_forward_chain_with_identity_stack(oracle):
+    """Zero out-projections and second linears make every transformer the
+    identity; the forward then reduces to the float64 numpy chain above, which
+    pins the composition's middle (band split -> final norm -> mask MLPs ->
+    merge).  The same chain without the final norm (a planted bug) must not
+    match."""
+    import csm_file
+    cfg = dict(SMALL_BSR, depth=2, zero_dc=True)
+    w = csm_file.bsr_checkpoint(cfg, seed=5)
+    _zero_branches(w, cfg["depth"])
+    x = rnd(1, 2, 64 * 30)
+    y = oracle.bsroformer_forward(cfg, w, x)
+    dims = [4 * f for f in cfg["freqs_per_bands"]]
+    L = cfg["mask_estimator_depth"]
+    r = _np_identity_forward(cfg, w, x, dims, None, [w["final_norm.gamma"]], L)
+    assert y.shape == r.shape
+    assert rel_err(y, r) < 1e-4
+    bug = _np_identity_forward(cfg, w, x, dims, None, [], L)
+    assert rel_err(y, bug) > 1e-2
+
+
+def test_melbandroformer_forward_chain_with_identity_stack(oracle):
+    """The MelBandRoformer chain with identity transformers: what remains of
+    the stack is the norm closing every transformer, in order (time then
+    frequency per depth), on overlapping bands whose masks are averaged per
+    bin.  Dropping one closing norm (a planted bug) must not match."""
+    import csm_file
+    cfg = dict(SMALL_MBR, depth=2, zero_dc=True)
+    fidx, counts = csm_file.overlapping_bands(129, 2, 16)
+    w = csm_file.mbr_checkpoint(cfg, counts, seed=6, precomputed=(fidx, counts))
+    _zero_branches(w, cfg["depth"])
+    x = rnd(1, 2, 64 * 30)
+    y = oracle.melbandroformer_forward(cfg, w, x)
+    dims = [4 * int(c) for c in counts]
+    norms = [w[f"layers.{d}.{t}.norm.gamma"] for d in range(2) for t in range(2)]
+    L = cfg["mask_estimator_depth"] + 1
+    r = _np_identity_forward(cfg, w, x, dims, fidx, norms, L)
+    assert y.shape == r.shape
+    assert rel_err(y, r) < 1e-4
+    bug = _np_identity_forward(cfg, w, x, dims, fidx, norms[:-1], L)
+    assert rel_err(y, bug) > 1e-2
