@@ -27,6 +27,14 @@ Prints ONE JSON line:
   pcie_inclusive_ms_per_chunk
                  the same step with the chunk handed over in pinned host
                  memory (H2D copy + stack + D2H copy); never `value`
+  config5_batch4 four chunks per step (M = 198648): ms per chunk = step / 4
+  config1_fp32_layer
+                 one MelBandRoformer time layer in fp32 on [60, 801, 384] and
+                 its fp32 kernels against the fp32 matrix peak
+  config2_gemm_sweep
+                 every (M, K, N, epilogue, dtype) of the GEMM sweep alone:
+                 TFLOP/s and fraction of the matrix peak, or GB/s and the
+                 fraction of HBM peak for the N = 8 gate projection
 """
 from __future__ import annotations
 
@@ -43,6 +51,7 @@ PKG_DIR = os.path.join(ROOT, "cuda-msst-infer_amd")
 
 METRIC = "ms per 8s chunk + GEMM TFLOP/s (% MFMA peak), BSRoformer fp16, 1×MI355X"
 PEAK_F16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, published
+PEAK_F32_TFLOPS = 157.3    # MI355X fp32 matrix, published
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, published
 
 # BSRoformer config: [62 bands, 801 frames] per 8 s chunk (44.1 kHz, hop 441).
@@ -157,6 +166,150 @@ def gemm_replay(msst, torch, layers, batch):
     return run
 
 
+def host_cpu_model():
+    """The host CPU's model name (lscpu 'Model name', else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def batch4_stack(msst, torch, layers, final_gamma, steps):
+    """Config 5: four overlapped 8 s chunks in one step (time layers on
+    [248, 801, 512], frequency layers on [3204, 62, 512], M = 198648);
+    ms per chunk = step time / 4, and the GEMM replay at the same M."""
+    B = 4
+    st = msst.RoformerStack(layers, final_gamma, B, FRAMES, BANDS, DIM, HEADS, DH, FF, msst.F16)
+    x = torch.randn(B, FRAMES, BANDS, DIM, device="cuda",
+                    generator=torch.Generator(device="cuda").manual_seed(4))
+    for _ in range(2):
+        st(x)
+    ms = time_events(torch, lambda: st(x), steps) / steps
+    assert torch.isfinite(x).all().item(), "non-finite batched stack output"
+    run = gemm_replay(msst, torch, layers, B)
+    run()
+    gms = time_events(torch, run, 2) / 2
+    M = B * FRAMES * BANDS
+    gflops = gemm_flops_per_token_layer() * M * 2 * DEPTH
+    tf = gflops / (gms * 1e-3) / 1e12
+    return {"ms_per_step": round(ms, 3), "ms_per_chunk": round(ms / B, 3),
+            "gemm_ms_per_chunk": round(gms / B, 3), "gemm_tflops": round(tf, 1),
+            "gemm_frac_of_peak": round(tf / PEAK_F16_TFLOPS, 4),
+            "stack_tflops": round((gflops + attn_flops_chunk(B)) / (ms * 1e-3) / 1e12, 1),
+            "config": "BSRoformer stack, 4 chunks per step (time layers on [248, 801, 512], "
+                      "frequency layers on [3204, 62, 512], M = 198648), depth 12, fp16"}
+
+
+def gemm_sweep(msst, torch):
+    """Config 2: every (M, K, N, epilogue, dtype) of the sweep, each GEMM
+    HIP-event timed alone (10 launches after one warm-up).  fp16: x, W fp16,
+    fp32 accumulation, fp16 out; fp32: x, W, out fp32 (true fp32 MFMA).
+    Bias ~ N(0, 0.02), A ~ N(0, 1), W ~ N(0, 0.02).  MFMA-bound shapes
+    report TFLOP/s and the fraction of the dtype's matrix peak; N = 8 (the
+    gate projection) is HBM-bound and reports GB/s of its algorithmic bytes
+    (A read once, W, bias, out written once) and the fraction of HBM peak."""
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    out = []
+    shapes = [(384, 1536), (1536, 384), (512, 1536), (512, 2048), (2048, 512), (384, 8), (512, 8)]
+    for M in (48060, 49662, 198648):
+        for K, N in shapes:
+            a32 = torch.randn(M, K, device="cuda", generator=gen)
+            w32 = torch.randn(N, K, device="cuda", generator=gen) * 0.02
+            b = torch.randn(N, device="cuda", generator=gen) * 0.02
+            for dt in ("f16", "f32"):
+                tdt = torch.float16 if dt == "f16" else torch.float32
+                a, w = a32.to(tdt), w32.to(tdt)
+                o = torch.empty(M, N, device="cuda", dtype=tdt)
+                for epi in ("none", "gelu", "sigmoid"):
+                    fn = lambda: msst.linear(a, w, b, epi, out=o)
+                    fn()
+                    us = time_events(torch, fn, 10) / 10 * 1e3
+                    flops = 2.0 * M * K * N
+                    eb = 2 if dt == "f16" else 4
+                    nbytes = eb * (M * K + N * K + M * N) + 4 * N
+                    e = {"M": M, "K": K, "N": N, "epilogue": epi, "dtype": dt,
+                         "us": round(us, 2), "tflops": round(flops / (us * 1e-6) / 1e12, 1)}
+                    if N <= 16:
+                        gbs = nbytes / (us * 1e-6) / 1e9
+                        e.update({"bound": "hbm", "gbs": round(gbs, 1),
+                                  "frac_hbm": round(gbs / PEAK_HBM_GBS, 4)})
+                    else:
+                        peak = PEAK_F16_TFLOPS if dt == "f16" else PEAK_F32_TFLOPS
+                        e.update({"bound": "mfma", "frac_mfma": round(e["tflops"] / peak, 4)})
+                    out.append(e)
+            del a32, w32, a, w, o
+    torch.cuda.empty_cache()
+    return out
+
+
+def config1_fp32_layer(msst, torch):
+    """Config 1 on the GPU: one MelBandRoformer time layer in fp32 on
+    x [60, 801, 384] (fp32 weights ~ N(0, 0.02), true fp32 MFMA), the whole
+    layer HIP-event timed, and each fp32 kernel alone against the fp32
+    matrix peak (the attention's QK^T + PV flops as MFMA work)."""
+    F, T, dim, heads, ff = 60, 801, 384, 8, 1536
+    hd = heads * DH
+    g = torch.Generator(device="cuda").manual_seed(11)
+
+    def n(*sh):
+        return torch.randn(*sh, device="cuda", generator=g) * 0.02
+
+    def gm():
+        return 1.0 + torch.randn(dim, device="cuda", generator=g) * 0.02
+
+    lw = dict(attn_gamma=gm(), w_qkv=n(3 * hd, dim), w_gate=n(heads, dim), b_gate=n(heads),
+              w_out=n(dim, hd), ff_gamma=gm(), w_ff1=n(ff, dim), b_ff1=n(ff), w_ff2=n(dim, ff),
+              b_ff2=n(dim))
+    st = msst.RoformerStack([lw, lw], None, 1, T, F, dim, heads, DH, ff, msst.F32)
+    x = torch.randn(F, T, dim, device="cuda", generator=g)
+    st.transformer(x, 0, 0)
+    layer_ms = time_events(torch, lambda: st.transformer(x, 0, 0), 5) / 5
+    M = F * T
+    gemm_flops = 2.0 * M * (dim * 3 * hd + hd * dim + dim * ff + ff * dim)
+    att_flops = 4.0 * F * heads * T * T * DH
+    xn = torch.randn(M, dim, device="cuda", generator=g)
+    merged = torch.randn(M, hd, device="cuda", generator=g)
+    qkv = torch.empty(M, 3 * hd, device="cuda")
+    hid = torch.empty(M, ff, device="cuda")
+    res = torch.randn(M, dim, device="cuda", generator=g)
+    q, k, v = (torch.randn(F, heads, T, DH, device="cuda", generator=g) for _ in range(3))
+    kern = {}
+    for name, fn, flops in (
+            ("gemm_qkv", lambda: msst.linear(xn, lw["w_qkv"], out=qkv), 2.0 * M * dim * 3 * hd),
+            ("gemm_out_residual", lambda: msst.linear(merged, lw["w_out"], residual=res, out=res),
+             2.0 * M * hd * dim),
+            ("gemm_ff1_gelu", lambda: msst.linear(xn, lw["w_ff1"], lw["b_ff1"], "gelu", out=hid),
+             2.0 * M * dim * ff),
+            ("gemm_ff2_residual", lambda: msst.linear(hid, lw["w_ff2"], lw["b_ff2"],
+                                                      residual=res, out=res), 2.0 * M * ff * dim),
+            ("attention", lambda: msst.attention(q, k, v), att_flops)):
+        fn()
+        us = time_events(torch, fn, 10) / 10 * 1e3
+        tf = flops / (us * 1e-6) / 1e12
+        kern[name] = {"us": round(us, 1), "tflops": round(tf, 1),
+                      "frac_fp32_peak": round(tf / PEAK_F32_TFLOPS, 4)}
+    gemm_us = sum(kern[k]["us"] for k in kern if k.startswith("gemm"))
+    return {"layer_ms": round(layer_ms, 3),
+            "layer_tflops": round((gemm_flops + att_flops) / (layer_ms * 1e-3) / 1e12, 1),
+            "gemm_tflops": round(gemm_flops / (gemm_us * 1e-6) / 1e12, 1),
+            "gemm_frac_fp32_peak": round(gemm_flops / (gemm_us * 1e-6) / 1e12 / PEAK_F32_TFLOPS, 4),
+            "kernels": kern,
+            "config": "MelBandRoformer time layer, fp32 weights and activations, x [60, 801, 384], "
+                      "8 heads x 64, FF 1536 GELU; peak: fp32 matrix 157.3 TFLOP/s"}
+
+
 def cpu_baseline_and_parity(msst, torch, args):
     """Oracle on the whole workload (one 8 s chunk through the 12-depth
     stack, BSRoformer final norm) with its own seeded weights — about 10 s of
@@ -197,7 +350,7 @@ def cpu_baseline_and_parity(msst, torch, args):
     y = xd.cpu().numpy().astype(np.float64)
     err = float(np.max(np.abs(y - ref)) / np.max(np.abs(ref)))
     cpu = {"value": round(cpu_s * 1e3, 1), "unit": "ms/chunk", "cores": threads,
-           "kind": "port",
+           "cpu_model": host_cpu_model(), "kind": "port",
            "sample": "fp32 C oracle (OpenMP), one whole 8 s chunk: the 12-depth stack with "
                      "final norm at full size [801 frames x 62 bands x 512], "
                      f"measured {cpu_s:.2f} s"}
@@ -372,6 +525,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=1, help="chunks per step (config 5 uses 4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations' sections (batch of 4 chunks, fp32 "
+                         "layer, GEMM sweep)")
     ap.add_argument("--pmc-sample", nargs="?", const="ff1", choices=("ff1", "kernels"),
                     help="run only the copy-kernel calibration and then the FF1 GEMM (ff1) or "
                          "every kernel of one transformer (kernels), 3 launches each, for "
@@ -486,6 +642,11 @@ def main():
     # one stem's mask estimator on the same chunk.
     out["bands"] = band_table(msst, torch, B)
     out["mbr_stack"] = mbr_stack_time(msst, torch, max(2, min(10, args.steps)))
+    if not args.no_configs:
+        out["config5_batch4"] = batch4_stack(msst, torch, layers, final_gamma,
+                                             max(2, min(5, args.steps)))
+        out["config1_fp32_layer"] = config1_fp32_layer(msst, torch)
+        out["config2_gemm_sweep"] = gemm_sweep(msst, torch)
     if not args.no_cpu:
         cpu, parity = cpu_baseline_and_parity(msst, torch, args)
         out["cpu_baseline"] = cpu
