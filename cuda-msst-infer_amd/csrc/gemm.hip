@@ -27,6 +27,7 @@
 // 8 XCDs, so workgroup b is given tile (b % 8) * per_xcd + b / 8 — every XCD
 // walks a contiguous run of the row-major tile grid and the column tiles of
 // a row block (which share the same A rows) run together in one L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "epilogue.hpp"
@@ -817,6 +818,131 @@ __global__ __launch_bounds__(kThreads) void gemm_skinny_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Skinny GEMM, vector form (N <= NP, K <= 64 * VA * S, 16-byte aligned rows):
+// HBM-bound.  One wave per row, two rows in flight; lane l covers the
+// 16-byte A slices l, l + 64, .. (VA elements each, S slices).  The lane's
+// slices of the N weight rows are loaded once and stay in
+// registers for every row the wave visits, so per row only the row itself
+// is read.  fp16 A and W use v_dot2_f32_f16 on packed pairs.  The N partial
+// dots go through gate_sums8 (8 at a time): sum n ends in lanes 8n .. 8n + 7
+// and lane 8n applies the bias (loaded once) and the activation and writes
+// output n.  The grid is sized so each wave sees many rows (the weight
+// loads are paid once per wave).
+// ---------------------------------------------------------------------------
+template <typename AT, typename WT, typename OutT, int NP, int S>
+__global__ __launch_bounds__(kThreads) void gemm_skinny_vec_kernel(
+    const AT* __restrict__ A, const WT* __restrict__ W, const float* __restrict__ bias,
+    const OutT* residual, OutT* out, int64_t M, int N, int K, int act) {
+    constexpr int VA = 16 / (int)sizeof(AT);
+    constexpr bool kDot2 = sizeof(AT) == 2 && sizeof(WT) == 2;
+    constexpr int WW = VA * (int)sizeof(WT) / 4;  // 32-bit words per weight slice: 2, 4 or 8
+    static_assert(NP == 8 || NP == 16, "NP");
+    const int lane = threadIdx.x & 63;
+    // Wave-uniform row index: keeps the buffer descriptors in SGPRs (a
+    // per-lane descriptor would need a waterfall loop around every load).
+    const int64_t wave = (int64_t)blockIdx.x * (kThreads / 64) +
+                         __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t nwaves = (int64_t)gridDim.x * (kThreads / 64);
+    // Weight slices: w[s][n] holds W[n, (s * 64 + lane) * VA ..][VA] as raw
+    // words, zero past N or K (buffer loads past the row read zero).
+    uint32_t w[S][NP][WW];
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<WT*>(W) + (n < N ? (int64_t)n * K : 0), (short)0,
+            n < N ? K * (int)sizeof(WT) : 0, 0x00020000);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int off = ((s * 64 + lane) * VA) * (int)sizeof(WT);
+            if constexpr (WW == 2) {
+                const u2v v = __builtin_bit_cast(u2v, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+                w[s][n][0] = v[0];
+                w[s][n][1] = v[1];
+            } else {
+#pragma unroll
+                for (int q = 0; q < WW / 4; ++q) {
+                    const u4v v = __builtin_bit_cast(
+                        u4v, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * q, 0, 0));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) w[s][n][4 * q + j] = v[j];
+                }
+            }
+        }
+    }
+    const int g = lane >> 3;
+    float bl[NP / 8];
+#pragma unroll
+    for (int h = 0; h < NP / 8; ++h) bl[h] = (bias && 8 * h + g < N) ? bias[8 * h + g] : 0.0f;
+
+    auto load_row = [&](int64_t row, u4v (&a)[S]) {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<AT*>(A) + (row < M ? row : 0) * K, (short)0,
+            row < M ? K * (int)sizeof(AT) : 0, 0x00020000);
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+            a[s] = __builtin_bit_cast(u4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                               r, ((s * 64 + lane) * VA) * (int)sizeof(AT), 0, 0));
+    };
+    auto wval = [&](int s, int n, int e) -> float {  // element e of weight slice (s, n)
+        if constexpr (sizeof(WT) == 2)
+            return (float)__builtin_bit_cast(h2, w[s][n][e / 2])[e % 2];
+        else
+            return __builtin_bit_cast(float, w[s][n][e]);
+    };
+    auto finish = [&](int64_t row, const u4v (&a)[S]) {
+        float acc[NP];
+#pragma unroll
+        for (int n = 0; n < NP; ++n) {
+            float d = 0.0f;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                if constexpr (kDot2) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        // Copy the vector element out first: clang's
+                        // __builtin_bit_cast of an ext_vector element lvalue
+                        // reads element 0 whatever the index.
+                        const uint32_t ae = a[s][e];
+                        d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, ae),
+                                                   __builtin_bit_cast(h2, w[s][n][e]), d, false);
+                    }
+                } else if constexpr (sizeof(AT) == 2) {
+                    const h8 x = __builtin_bit_cast(h8, a[s]);
+#pragma unroll
+                    for (int e = 0; e < VA; ++e) d = fmaf((float)x[e], wval(s, n, e), d);
+                } else {
+                    const f4 x = __builtin_bit_cast(f4, a[s]);
+#pragma unroll
+                    for (int e = 0; e < VA; ++e) d = fmaf(x[e], wval(s, n, e), d);
+                }
+            }
+            acc[n] = d;
+        }
+#pragma unroll
+        for (int h = 0; h < NP / 8; ++h) {
+            float part[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) part[i] = acc[8 * h + i];
+            const float tot = gate_sums8(part, lane);
+            const int n = 8 * h + g;
+            if ((lane & 7) == 0 && n < N && row < M) {
+                float v = act_apply(tot + bl[h], act);
+                const int64_t idx = row * (int64_t)N + n;
+                if (residual) v += (float)residual[idx];
+                out[idx] = (OutT)v;
+            }
+        }
+    };
+    u4v a0[S], a1[S];
+    for (int64_t row = wave; row < M; row += 2 * nwaves) {
+        load_row(row, a0);
+        load_row(row + nwaves, a1);
+        finish(row, a0);
+        finish(row + nwaves, a1);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Generic fallback: 16x16 output tile per 256-thread block, LDS-staged
 // 16-wide K slices, fp32 accumulation.  Correct for any M, N, K and dtype.
 // ---------------------------------------------------------------------------
@@ -994,6 +1120,24 @@ int launch_small(const void* x, const void* w, const float* bias, const OutT* re
         int64_t blocks = (M + 3) / 4;
         if (blocks > 8192) blocks = 8192;
         if (blocks < 1) blocks = 1;
+        constexpr int VA = 16 / (int)sizeof(AT);
+        const int slices = (K + 64 * VA - 1) / (64 * VA);
+        if (K % VA == 0 && aligned(x, 16) && aligned(w, 16) && slices <= 2) {
+            // Vector form: whole 16-byte A slices per lane, weights in
+            // registers; about 16 rows per wave (1024 blocks of 4 waves for
+            // M = 49662).
+            const int64_t vblocks = std::max<int64_t>(1, std::min<int64_t>((M + 63) / 64, 1024));
+#define MSST_SKV(NP, S)                                                                       \
+    hipLaunchKernelGGL((gemm_skinny_vec_kernel<AT, WT, OutT, NP, S>), dim3((unsigned)vblocks), \
+                       dim3(kThreads), 0, s, a, wt, bias, res, out, M, N, K, act)
+            if (N <= 8) {
+                if (slices == 1) MSST_SKV(8, 1); else MSST_SKV(8, 2);
+            } else {
+                if (slices == 1) MSST_SKV(16, 1); else MSST_SKV(16, 2);
+            }
+#undef MSST_SKV
+            return check_launch("gemm_skinny_vec_kernel");
+        }
         hipLaunchKernelGGL((gemm_skinny_kernel<AT, WT, OutT, 16>), dim3((unsigned)blocks),
                            dim3(kThreads), 0, s, a, wt, bias, res, out, M, N, K, act);
         return check_launch("gemm_skinny_kernel");

@@ -52,16 +52,20 @@ __device__ __forceinline__ f16x mfma32x32x2f32(float a, float b, f16x c) {
 // 7.1.26:
 //   1 - erf(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),
 //   t = 1 / (1 + p z), z >= 0,  |error| <= 1.5e-7.
-// With c = (1 - erf(|v| / sqrt 2)) / 2 (the polynomial's coefficients
-// halved, p folded with 1 / sqrt 2), v Phi(v) is v - v c for v >= 0 and
-// v c = -|v| c for v < 0: both are max(v, 0) - |v| c.  Thirteen VALU
-// operations (v_rcp_f32 and v_exp_f32 among them) against several times
-// that for the library erff, which dominated the FF1 epilogue; there is no
-// cancellation in 1 + erf for negative v, and the 0.75e-7 |v| absolute
-// error is far below the fp16 output rounding and the 1e-4 fp32 tolerance.
-// |v| is capped in the last product so that v = +inf gives +inf (c is 0
-// there), not inf * 0.
-// sigmoid / SiLU use the ROCm device-library expf.
+// With c = (1 - erf(|v| / sqrt 2)) / 2 = Phi(-|v|) (the polynomial's
+// coefficients halved, p folded with 1 / sqrt 2), v Phi(v) is v (1 - c) for
+// v >= 0 and v c for v < 0: both are v / 2 + |v| (1/2 - c), one FMA with
+// |v| as a free source modifier and no select, min or max (whose operands
+// the compiler would first canonicalise).  Fourteen VALU operations
+// (v_rcp_f32 and v_exp_f32 among them) against several times that for the
+// library erff, which dominated the FF1 epilogue.  Error: the approximation's
+// 0.75e-7 |v| plus the rounding of 1/2 - c (3e-8 |v|), far below the fp16
+// output rounding and the 1e-4 fp32 tolerance.  v = +inf gives +inf
+// (t = e = 0); v = -inf gives NaN, as v Phi(v) does.
+// sigmoid(v) = 1 / (1 + 2^(-v log2 e)) with v_exp_f32 and v_rcp_f32 (each
+// about 1 ulp): relative error ~3e-7 in 4 VALU operations instead of the
+// library expf and an IEEE division; v -> -inf gives rcp(inf) = 0, v -> +inf
+// gives 1.  SiLU = v sigmoid(v).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float gelu_erf(float v) {
     const float a = fabsf(v);
@@ -73,7 +77,11 @@ __device__ __forceinline__ float gelu_erf(float v) {
     // exp(-v^2 / 2) = 2^(-v^2 log2(e) / 2); v_exp_f32 flushes to 0 far out.
     const float e = __builtin_amdgcn_exp2f(v * (v * -0.72134752044448170f));
     const float c = (p * t) * e;
-    return fmaf(-fminf(a, 3.0e38f), c, fmaxf(v, 0.0f));
+    return fmaf(a, 0.5f - c, 0.5f * v);
+}
+
+__device__ __forceinline__ float sigmoid_fast(float v) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f));
 }
 
 // tanh(x) = (e^2x - 1) / (e^2x + 1) with e^2x from v_exp_f32 (|x| clamped to
@@ -98,9 +106,9 @@ __device__ __forceinline__ float act_fixed(float v) {
     if constexpr (ACT == MSST_ACT_GELU)
         return gelu_erf(v);
     else if constexpr (ACT == MSST_ACT_SIGMOID)
-        return 1.0f / (1.0f + expf(-v));
+        return sigmoid_fast(v);
     else if constexpr (ACT == MSST_ACT_SILU)
-        return v / (1.0f + expf(-v));
+        return v * sigmoid_fast(v);
     else
         return v;
 }
@@ -211,6 +219,38 @@ __device__ __forceinline__ float dpp_wave_sum(float v) {
     v += dpp_move<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
     v += dpp_move<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Eight per-lane partial sums (one per gate) reduced over the wave, with the
+// sum of gate g left in the eight lanes 8g .. 8g + 7.  Each step halves the
+// values a lane carries: the xor-32 and xor-16 exchanges pair two registers
+// through v_permlane32_swap / v_permlane16_swap (no selects needed), the
+// xor-8 one picks by lane bit 3 and moves by DPP row_ror:8; the last three
+// lane bits are summed with DPP (quad perms, row_half_mirror).  21 VALU
+// operations against 8 full wave sums.
+__device__ __forceinline__ float gate_sums8(const float (&v)[8], int lane) {
+    float c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // lane bit 5: values i (clear) / i + 4 (set)
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]),
+                                                        false, false);
+        c[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    float d[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // lane bit 4: + 0 / + 2
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(c[i]), __float_as_uint(c[i + 2]),
+                                                        false, false);
+        d[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const bool b3 = (lane & 8) != 0;  // lane bit 3: + 0 / + 1
+    const float keep = b3 ? d[1] : d[0];
+    const float send = b3 ? d[0] : d[1];
+    float s = keep + dpp_move<0x128, 0xF>(send);  // row_ror:8 = lane ^ 8 within a row
+    s += dpp_move<0xB1, 0xF>(s);   // quad_perm [1,0,3,2]
+    s += dpp_move<0x4E, 0xF>(s);   // quad_perm [2,3,0,1]
+    s += dpp_move<0x141, 0xF>(s);  // row_half_mirror
+    return s;
 }
 
 // Sum over the wave, the same value in every lane (all 64 lanes active).

@@ -74,38 +74,6 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[GP], int lane) {
     return s;
 }
 
-// Eight per-lane partial sums (one per gate) reduced over the wave, with the
-// sum of gate g left in the eight lanes 8g .. 8g + 7.  Each step halves the
-// values a lane carries: the xor-32 and xor-16 exchanges pair two registers
-// through v_permlane32_swap / v_permlane16_swap (no selects needed), the
-// xor-8 one picks by lane bit 3 and moves by DPP row_ror:8; the last three
-// lane bits are summed with DPP (quad perms, row_half_mirror).  21 VALU
-// operations against 8 full wave sums.
-__device__ __forceinline__ float gate_sums8(const float (&v)[8], int lane) {
-    float c[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {  // lane bit 5: values i (clear) / i + 4 (set)
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]),
-                                                        false, false);
-        c[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    float d[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {  // lane bit 4: + 0 / + 2
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(c[i]), __float_as_uint(c[i + 2]),
-                                                        false, false);
-        d[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    const bool b3 = (lane & 8) != 0;  // lane bit 3: + 0 / + 1
-    const float keep = b3 ? d[1] : d[0];
-    const float send = b3 ? d[0] : d[1];
-    float s = keep + dpp_move<0x128, 0xF>(send);  // row_ror:8 = lane ^ 8 within a row
-    s += dpp_move<0xB1, 0xF>(s);   // quad_perm [1,0,3,2]
-    s += dpp_move<0x4E, 0xF>(s);   // quad_perm [2,3,0,1]
-    s += dpp_move<0x141, 0xF>(s);  // row_half_mirror
-    return s;
-}
-
 template <typename XT, typename OutT, typename WT, int GP>
 __global__ __launch_bounds__(kThreads) void rms_norm_vec_kernel(
     const XT* __restrict__ x, const float* __restrict__ gamma, float scale,
@@ -160,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_vec_kernel(
             constexpr int SHIFT = GP == 16 ? 2 : 3;
             const int g = lane >> SHIFT;
             if ((lane & ((1 << SHIFT) - 1)) == 0 && g < G)
-                gates[row * G + g] = 1.0f / (1.0f + expf(-(s + bg[g])));
+                gates[row * G + g] = sigmoid_fast(s + bg[g]);
         }
     }
 }
@@ -270,7 +238,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_gate_h_kernel(
         }
         const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
             gates + (live ? row : 0) * G, (short)0, live ? G * 4 : 0, 0x00020000);
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(1.0f / (1.0f + expf(-(mine + bgl)))),
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sigmoid_fast(mine + bgl)),
                                               rg, goff, 0, 0);
     };
     // Two row buffers in turn: one row is processed while the next loads.
@@ -336,7 +304,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_scalar_kernel(
             constexpr int SHIFT = GP == 16 ? 2 : 3;
             const int g = lane >> SHIFT;
             if ((lane & ((1 << SHIFT) - 1)) == 0 && g < G)
-                gates[row * G + g] = 1.0f / (1.0f + expf(-(s + bg[g])));
+                gates[row * G + g] = sigmoid_fast(s + bg[g]);
         }
     }
 }

@@ -79,7 +79,10 @@ def test_rms_norm_gate(msst, oracle, cuda, rows, D, G, dt):
 
 # ------------------------------------------------------------------ linear
 SMALL = [(1, 64, 32), (31, 64, 8), (100, 384, 1536), (257, 512, 512), (1000, 72, 100),
-         (300, 2048, 384), (65, 50, 40), (600, 512, 8), (40, 136, 264)]
+         (300, 2048, 384), (65, 50, 40), (600, 512, 8), (40, 136, 264),
+         # N <= 16: vector skinny kernel (1 or 2 slices of 16 bytes per lane) and
+         # the scalar fallback (K not a multiple of the vector, or longer rows)
+         (333, 1000, 12), (77, 1024, 16), (5, 24, 3), (50, 100, 5), (129, 2000, 8), (2, 384, 1)]
 
 
 @pytest.mark.parametrize("M,K,N", SMALL)
