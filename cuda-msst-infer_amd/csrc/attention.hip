@@ -28,7 +28,8 @@
 // waves take 4 consecutive 64-query tiles of one (sequence, head) and share
 // double-buffered K/V blocks; HPW = 4 for sequences of <= 64 positions —
 // each wave owns one head of the sequence.  Workgroup ids are dealt
-// XCD-aware (see gemm.hip) so the query tiles of one head share an L2.
+// XCD-aware (work_item) so the query tiles of one head share an L2, with
+// mostly idle last q-tiles dispatched after all full ones.
 //
 // RoPE (ops_misc.cu:39-69, interleaved pairs) is applied in fp32 while Q and
 // K are staged; the gate (ops_fused.cu:285-303 output) multiplies the
@@ -61,7 +62,8 @@ struct AttnParams {
     int H;
     int qtiles;                 // 64*waves_per_head-query tiles per (seq, head)
     int64_t total_items;        // workgroup work items
-    int per_xcd;
+    int per_xcd;                // work items per XCD (see work_item)
+    int short_last;             // most waves of a pair's last q-tile are idle
     float scale_log2;           // softmax scale * log2(e)
 };
 
@@ -90,9 +92,42 @@ __device__ __forceinline__ int swap_bits23(int kr) {
     return (kr & ~0xC) | ((kr & 4) << 1) | ((kr & 8) >> 1);
 }
 
-__device__ __forceinline__ void work_item(const AttnParams& p, int64_t& item) {
+// Work item of this workgroup: (sequence, head group) pair sh and q-tile
+// qt.  Workgroups are dealt round-robin to the 8 XCDs (workgroup b runs on
+// XCD b % 8), so XCD x is given a contiguous run of the items and walks it
+// in dispatch order b / 8; the q-tiles of one pair are adjacent, so they
+// run together and share K/V in that XCD's L2.  When most waves of the last
+// q-tile of a pair are idle (p.short_last), XCD x is given the pairs
+// [x per, x per + per) and walks first every q-tile but the last of each
+// pair, then the last q-tile of each: the short workgroups fill the end of
+// the grid instead of holding workgroup slots beside full ones.  Returns
+// false for the grid's padding workgroups.
+__device__ __forceinline__ bool work_item(const AttnParams& p, int64_t& sh, int& qt) {
     const int64_t b = blockIdx.x;
-    item = (b & 7) * (int64_t)p.per_xcd + (b >> 3);
+    const int64_t l = b >> 3;
+    const int Q = p.qtiles;
+    if (!p.short_last) {
+        const int64_t item = (b & 7) * (int64_t)p.per_xcd + l;
+        if (item >= p.total_items) return false;
+        sh = item / Q;
+        qt = (int)(item % Q);
+        return true;
+    }
+    const int64_t S = p.total_items / Q;
+    const int64_t per = (S + 7) / 8;
+    const int64_t base = (b & 7) * per;
+    const int64_t n = min(per, S - base);
+    if (n <= 0) return false;
+    if (l < n * (Q - 1)) {
+        sh = base + l / (Q - 1);
+        qt = (int)(l % (Q - 1));
+    } else if (l < n * Q) {
+        sh = base + (l - n * (Q - 1));
+        qt = Q - 1;
+    } else {
+        return false;
+    }
+    return true;
 }
 
 // ===========================================================================
@@ -107,17 +142,14 @@ __global__ __launch_bounds__(256) void attn_f16_kernel(AttnParams p) {
     constexpr int CH = kKB * 8 / GROUP;   // 16-byte chunks per thread per tensor
     __shared__ __attribute__((aligned(16))) half_t lds[NSLOT * SLOT];
 
-    int64_t item;
-    work_item(p, item);
-    if (item >= p.total_items) return;
+    int64_t sh;
+    int qt_idx;
+    if (!work_item(p, sh, qt_idx)) return;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int lrow = lane & 31, lh = lane >> 5;
     const int head_local = w / WPH, qsub = w % WPH;
-    // item = (seq * head_groups + hg) * qtiles + qt
     const int head_groups = (p.H + HPW - 1) / HPW;
-    const int qt_idx = (int)(item % p.qtiles);
-    const int64_t sh = item / p.qtiles;
     const int hg = (int)(sh % head_groups);
     const int64_t seq = sh / head_groups;
     const int h = hg * HPW + head_local;
@@ -398,17 +430,15 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
     constexpr int NDMA = 2 * ROWS_W / 8;        // DMA instructions per wave per block
     __shared__ __attribute__((aligned(16))) half_t lds[NSLOT * SLOT];
 
-    int64_t item;
-    work_item(p, item);
-    if (item >= p.total_items) return;
+    int64_t sh;
+    int qt_idx;
+    if (!work_item(p, sh, qt_idx)) return;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lrow = lane & 31, lh = lane >> 5;
     const int head_local = w / WPH, qsub = w % WPH;
     const int head_groups = (p.H + HPW - 1) / HPW;
-    const int qt_idx = (int)(item % p.qtiles);
-    const int64_t sh = item / p.qtiles;
     const int hg = (int)(sh % head_groups);
     const int64_t seq = sh / head_groups;
     const int h = hg * HPW + head_local;
@@ -630,16 +660,14 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnParams p) {
     constexpr int CH = kKB * 16 / GROUP;  // 16-byte chunks (4 floats) per thread
     extern __shared__ __attribute__((aligned(16))) float lds_f[];
 
-    int64_t item;
-    work_item(p, item);
-    if (item >= p.total_items) return;
+    int64_t sh;
+    int qt_idx;
+    if (!work_item(p, sh, qt_idx)) return;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int lrow = lane & 31, lh = lane >> 5;
     const int head_local = w / WPH, qsub = w % WPH;
     const int head_groups = (p.H + HPW - 1) / HPW;
-    const int qt_idx = (int)(item % p.qtiles);
-    const int64_t sh = item / p.qtiles;
     const int hg = (int)(sh % head_groups);
     const int64_t seq = sh / head_groups;
     const int h = hg * HPW + head_local;
@@ -850,9 +878,17 @@ int launch_attention(AttnParams& p, int64_t n_seq, int dtype, hipStream_t s) {
     p.qtiles = (p.n_q + 64 * wph - 1) / (64 * wph);
     const int64_t head_groups = (p.H + hpw - 1) / hpw;
     p.total_items = n_seq * head_groups * p.qtiles;
-    p.per_xcd = (int)((p.total_items + 7) / 8);
-    const int64_t grid = (int64_t)p.per_xcd * 8;
-    if (grid > 0x7fffffff) return set_error(MSST_ERR_UNSUPPORTED, "attention grid too large");
+    // A q-tile covers 64 * wph queries (64 per wave); the last one is
+    // reordered when at least half of its waves are idle (with fewer, the
+    // q-tiles of a pair running together in one L2 is worth more).
+    p.short_last = p.qtiles * 64 * wph - p.n_q >= 32 * wph ? 1 : 0;
+    // Grid: 8 XCDs x work items per XCD (whole pairs per XCD when the last
+    // q-tiles are reordered, see work_item).
+    const int64_t per_xcd = p.short_last ? (n_seq * head_groups + 7) / 8 * p.qtiles
+                                         : (p.total_items + 7) / 8;
+    if (per_xcd > 0x7fffffff / 8) return set_error(MSST_ERR_UNSUPPORTED, "attention grid too large");
+    p.per_xcd = (int)per_xcd;
+    const int64_t grid = per_xcd * 8;
     if (dtype == MSST_F16 && p.cos_t == nullptr && dma_fits(p)) {
         if (hpw == 4)
             hipLaunchKernelGGL(attn_f16_dma_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, p);
@@ -919,14 +955,21 @@ extern "C" int msst_attention(const void* q, const void* k, const void* v, void*
     if (scale == 0.0f) scale = 1.0f / sqrtf((float)D);
     AttnParams p{};
     p.q = q; p.k = k; p.v = v; p.out = out;
-    p.ld_in = D; p.ld_out = D; p.head_in = 0; p.head_out = 0;
+    p.ld_in = D; p.ld_out = D;
     p.cos_t = nullptr; p.sin_t = nullptr; p.gates = nullptr;
     p.n_inner = 1;
-    p.q_outer = N; p.q_inner = 0; p.q_pos = 1;
-    p.k_outer = Nk; p.k_inner = 0; p.k_pos = 1;
-    p.n_q = (int)N; p.n_k = (int)Nk; p.H = 1;
+    p.n_q = (int)N; p.n_k = (int)Nk;
     p.scale_log2 = scale * kLog2e;
-    return launch_attention(p, B * H, dtype, as_stream(stream));
+    // [B, H, N, D] as B sequences of H heads (head h of batch b at element
+    // (b H + h) N D), so short sequences take the four-heads-per-workgroup
+    // form; q and k/v share one head stride, so N != Nk runs B * H
+    // one-head sequences instead.
+    const bool heads = N == Nk && H <= (1 << 30);
+    p.H = heads ? (int)H : 1;
+    p.head_in = p.head_out = heads ? N * D : 0;
+    p.q_outer = heads ? H * N : N; p.q_inner = 0; p.q_pos = 1;
+    p.k_outer = heads ? H * Nk : Nk; p.k_inner = 0; p.k_pos = 1;
+    return launch_attention(p, heads ? B : B * H, dtype, as_stream(stream));
 }
 
 extern "C" int msst_gated_rope_attention(const void* qkv, int dtype, int64_t ld_qkv,
