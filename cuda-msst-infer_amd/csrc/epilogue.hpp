@@ -1,6 +1,6 @@
-// epilogue.hpp — GEMM epilogue shared by the GEMM kernels (gemm.hip) and
-// the fused feed-forward kernel (ffn.hip): LDS-staged, row-contiguous stores
-// with bias, activation, residual or RoPE applied on the way out.
+// epilogue.hpp — epilogue of the MFMA GEMM kernels (gemm.hip): LDS-staged,
+// row-contiguous stores with bias, activation, residual or RoPE applied on
+// the way out.
 #pragma once
 
 #include "msst_common.hpp"

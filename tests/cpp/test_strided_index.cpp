@@ -3,6 +3,7 @@
 // hardware division, and the axis merge against a plain multi-axis walk,
 // by replaying the kernels' per-unit offset computation on the host.
 // Exit status 0 and a last line "OK" when every check passes.
+#include <algorithm>
 #include <cstdio>
 #include <random>
 #include <vector>
