@@ -1186,6 +1186,19 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
             // (The activation kernels start their accumulators from 16-byte
             // bias loads, which need N % 4 == 0; other N take the
             // register-staged kernel below.)
+            // 128 x 128 tiles at three workgroups per CU also take:
+            //  - launches with fewer 256 x 256 tiles than CUs (small M):
+            //    M = 1000, K = N = 512 with residual 22 -> 8.5 us;
+            //  - the K <= 512 residual GEMM (the out-projection): its
+            //    epilogue residual then streams beside other workgroups'
+            //    main loops (58.5 against 61 us alone; BSRoformer chunk
+            //    15.28 -> 15.23 ms, MelBandRoformer 6.19 -> 6.16 ms, A/B
+            //    in the stack on one box).
+            const bool small = ((M + 255) / 256) * ((N + 255) / 256) < 256;
+            const bool narrow_res = res != nullptr && K <= 512;
+            if (act == MSST_ACT_NONE && (small || narrow_res) && N % 4 == 0)
+                return launch_f16_dma<128, 128, 32, 3, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act,
+                                                                   s);
             if (act == MSST_ACT_NONE && N % 256 == 0 && (!res || std::is_same<OutT, float>::value))
                 return launch_pp<32, 3, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
             if (act != MSST_ACT_NONE && N % 4 == 0)
@@ -1274,6 +1287,12 @@ extern "C" int msst_linear_rope(const void* x, const void* w, const float* bias,
     const half_t* xh = reinterpret_cast<const half_t*>(x);
     const half_t* wh = reinterpret_cast<const half_t*>(w);
     half_t* oh = reinterpret_cast<half_t*>(out);
+    // Fewer 256 x 256 tiles than CUs (small M): 128 x 128 tiles at three
+    // workgroups per CU (the 64-column wave tiles divide the RoPE columns).
+    if (((M + 255) / 256) * ((N + 255) / 256) < 256)
+        return launch_f16_dma<128, 128, 32, 3, 3, 2, half_t>(xh, wh, bias, nullptr, oh, (int)M,
+                                                             (int)N, (int)K, MSST_ACT_NONE,
+                                                             as_stream(stream), &r);
     if (N % 256 == 0)
         return launch_pp<32, 3, half_t>(xh, wh, bias, nullptr, oh, (int)M, (int)N, (int)K,
                                         MSST_ACT_NONE, as_stream(stream), &r);
