@@ -378,9 +378,12 @@ __global__ __launch_bounds__(256) void attn_f16_kernel(AttnParams p) {
 // sums add the fp16 P values the PV MFMA consumes (v_dot2 against 1.0), so
 // numerator and denominator see the same rounding.  The lane ^ 32 partner
 // of a query's scores is reached with v_permlane32_swap.
-// Schedule: a 64-key block is two 32-key halves.  S of half 1 is issued
-// while the softmax of half 0 runs on the VALU, and PV of half 0 while the
-// softmax of half 1 runs, so MFMA and VALU work of one wave overlap.
+// Schedule: a 64-key block is two 32-key halves, each run S -> softmax ->
+// PV in turn, so only one half's scores and P are live: the HPW = 1 kernel
+// fits 168 VGPRs and runs three workgroups (12 waves) per CU, whose waves
+// overlap one another's MFMA and VALU phases.  (Issuing S of half 1 ahead
+// of half 0's softmax, for overlap within a wave, needed ~200 VGPRs, two
+// workgroups per CU, and ran 9-15 % slower.)
 // HPW = 1: 4 waves x 64 queries of one (sequence, head) share a 3-stage K/V
 // ring (each wave DMAs 16 of the 64 rows; fence-free barrier, one block of
 // DMA in flight per wave while a block computes).  HPW = 4 (<= 64 keys):
@@ -393,25 +396,24 @@ __device__ __forceinline__ h4 lds_read_tr16(const lds_half_t* ptr) {
     return __builtin_bit_cast(h4, v);
 }
 
-// Plain v_max: the scores come from MFMA accumulators (never signalling
-// NaNs), and fmaxf in IEEE mode would first canonicalise every input with
-// an extra v_max x, x.
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
+// Maxima of scores: llvm.maximum, which gfx950 lowers to v_maximum3_f32
+// / v_maximum_f32 (NaN-propagating) with no input canonicalisation, where
+// fmaxf in IEEE mode would first quiet every input with an extra
+// v_max x, x.  Being compiler-visible (not inline asm), these reads of MFMA
+// accumulators get the MFMA-to-VALU wait states from the compiler's hazard
+// tracking, which does not look inside inline asm.
+__device__ __forceinline__ float fmax_nc(float a, float b) {
+    return __builtin_elementwise_maximum(a, b);
 }
-__device__ __forceinline__ float vmax(float a, float b) {
-    float r;
-    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-    return r;
+__device__ __forceinline__ float fmax3_nc(float a, float b, float c) {
+    return fmax_nc(fmax_nc(a, b), c);
 }
 
 // max over the query's two lanes (l, l ^ 32).
 __device__ __forceinline__ float pair_max(float a) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false,
                                                     false);
-    return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return fmax_nc(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float pair_sum(float a) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false,
@@ -422,7 +424,7 @@ __device__ __forceinline__ float pair_sum(float a) {
 constexpr float kRescaleLog2 = 8.0f;
 
 template <int HPW>
-__global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(AttnParams p) {
     constexpr int WPH = 4 / HPW;
     constexpr int NSLOT = HPW == 1 ? 3 : 4;
     constexpr int SLOT = 2 * kKB * kD;          // halves: K tile, then V tile
@@ -536,10 +538,10 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
                 for (int v = 0; v < 16; ++v)
                     if (8 * (v >> 2) + (v & 3) >= lim) shf[qt][v] = -INFINITY;
             }
-            float m = vmax3(shf[qt][0], shf[qt][1], shf[qt][2]);
+            float m = fmax3_nc(shf[qt][0], shf[qt][1], shf[qt][2]);
 #pragma unroll
-            for (int v = 3; v < 15; v += 2) m = vmax3(m, shf[qt][v], shf[qt][v + 1]);
-            const float mx = pair_max(vmax(m, shf[qt][15]));
+            for (int v = 3; v < 15; v += 2) m = fmax3_nc(m, shf[qt][v], shf[qt][v + 1]);
+            const float mx = pair_max(fmax_nc(m, shf[qt][15]));
             if (mx > m_run[qt] + th) {
                 const float alpha = __builtin_amdgcn_exp2f((m_run[qt] - mx) * c);
                 m_run[qt] = mx;
@@ -584,9 +586,9 @@ __global__ __launch_bounds__(256, 2) void attn_f16_dma_kernel(AttnParams p) {
         f16x sa[2], sb[2];
         h8 pa[2][2], pb[2][2];
         s_half(Ks, 0, sa);
-        s_half(Ks, 1, sb);                      // overlaps softmax of half 0
         softmax_half(tail_c, key_base, sa, pa);
-        pv_half(Ks, 0, pa);                     // overlaps softmax of half 1
+        pv_half(Ks, 0, pa);
+        s_half(Ks, 1, sb);
         softmax_half(tail_c, key_base + 32, sb, pb);
         pv_half(Ks, 1, pb);
     };

@@ -336,6 +336,26 @@ def test_attention_rising_scores(msst, oracle, cuda, N, growth, dt):
     assert rel_err(host(y), r) < tol(dt)
 
 
+@pytest.mark.parametrize("dt,B,N", [("f16", 62, 801), ("f16", 801, 62), ("f32", 30, 801)])
+def test_attention_deterministic(msst, cuda, dt, B, N):
+    """Bitwise-equal outputs across reruns, and for B sequences alone versus
+    as the first B of a 4x larger batch: each output row depends only on its
+    own (sequence, head), so any difference is a race inside the kernel
+    (e.g. a VALU read of an MFMA accumulator before the MFMA has finished,
+    which perturbs the running maximum and so the fp16 probabilities by an
+    ulp).  The shapes are the time-axis (801 keys, three-stage K/V ring) and
+    frequency-axis (62 keys, one block per wave) cases of the model."""
+    g = torch.Generator(device="cuda").manual_seed(N)
+    q, k, v = (torch.randn(4 * B, 8, N, 64, device="cuda", generator=g).to(tdt(dt))
+               for _ in range(3))
+    y4 = msst.attention(q, k, v)
+    y1 = msst.attention(q[:B], k[:B], v[:B])
+    reruns = [msst.attention(q[:B], k[:B], v[:B]) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert torch.equal(y4[:B], y1)
+    assert all(torch.equal(y, y1) for y in reruns)
+
+
 # ------------------------------------------------------- fused QKV + RoPE
 def _rope_rows(oracle, y, c, s, B, F, T, H, axis, rope_cols):
     """Apply the oracle RoPE to columns [0, rope_cols) of token rows y in
