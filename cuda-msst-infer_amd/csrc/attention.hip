@@ -385,8 +385,8 @@ __global__ __launch_bounds__(256) void attn_f16_kernel(AttnParams p) {
 // of half 0's softmax, for overlap within a wave, needed ~200 VGPRs, two
 // workgroups per CU, and ran 9-15 % slower.)
 // HPW = 1: 4 waves x 64 queries of one (sequence, head) share a 3-stage K/V
-// ring (each wave DMAs 16 of the 64 rows; fence-free barrier, one block of
-// DMA in flight per wave while a block computes).  HPW = 4 (<= 64 keys):
+// ring (each wave DMAs 16 of the 64 rows; fence-free barrier; the next two
+// blocks in flight while a block computes).  HPW = 4 (<= 64 keys):
 // each wave owns one head and DMAs its own single block.
 typedef short s4_t __attribute__((__vector_size__(4 * sizeof(short))));
 typedef __attribute__((address_space(3))) s4_t lds_s4_t;
@@ -394,6 +394,39 @@ typedef __attribute__((address_space(3))) s4_t lds_s4_t;
 __device__ __forceinline__ h4 lds_read_tr16(const lds_half_t* ptr) {
     const s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)(ptr));
     return __builtin_bit_cast(h4, v);
+}
+
+// V^T fragment reads for the unrolled K/V ring, as inline asm.  The
+// compiler treats any LDS read it can see as possibly aliasing the ring's
+// in-flight LDS DMAs and waits for all of them (vmcnt(0)) first, which
+// would wait for the block prefetched two blocks ahead.  So the reads are
+// issued by asm (invisible to that analysis) and completed by an asm
+// lgkmcnt wait tied to their registers, so no user is scheduled above it.
+//
+// Issue (no wait) the four transposed reads of two V^T fragments at
+// a0 + OFF and a1 + OFF (rows r and r + 8 each).
+template <int OFF>
+__device__ __forceinline__ void lds_read_tr16_issue4(uint32_t a0, uint32_t a1, s4_t (&r)[4]) {
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %4 offset:%6\n\t"
+        "ds_read_b64_tr_b16 %1, %4 offset:%7\n\t"
+        "ds_read_b64_tr_b16 %2, %5 offset:%6\n\t"
+        "ds_read_b64_tr_b16 %3, %5 offset:%7"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+        : "v"(a0), "v"(a1), "n"(OFF), "n"(OFF + 8 * kD * 2));
+}
+// Wait until at most N LDS operations are outstanding.  LDS operations
+// complete in issue order, and any other LDS or scalar-memory operation the
+// compiler issues in between only adds to the count, so with N = the reads
+// issued after those needed, the wait can only be stricter than required.
+// The registers are tied to the wait so their users cannot move above it.
+template <int N>
+__device__ __forceinline__ void lds_wait_tied(s4_t (&r)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]) : "n"(N));
+}
+__device__ __forceinline__ h8 cat_h8(const s4_t& lo, const s4_t& hi) {
+    return __builtin_shufflevector(__builtin_bit_cast(h4, lo), __builtin_bit_cast(h4, hi), 0, 1, 2,
+                                   3, 4, 5, 6, 7);
 }
 
 // Maxima of scores: llvm.maximum, which gfx950 lowers to v_maximum3_f32
@@ -474,8 +507,7 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
     auto slot_ptr = [&](int kb) -> lds_half_t* {
         return L + (HPW == 1 ? (kb % NSLOT) : head_local) * SLOT;
     };
-    auto issue = [&](int kb) {
-        lds_half_t* Ks = slot_ptr(kb);
+    auto issue = [&](lds_half_t* Ks, int kb) {
         lds_half_t* Vs = Ks + kKB * kD;
 #pragma unroll
         for (int i = 0; i < ROWS_W / 8; ++i) {
@@ -582,23 +614,61 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
                 o[1][dm] = mfma32x32x16(vf, pf[1][tp], o[1][dm]);
             }
     };
-    auto block = [&](auto tail_c, const lds_half_t* Ks, int key_base) {
+    // The same with the slot S and half HF known at compile time: the V^T
+    // fragment reads take two per-lane base addresses and immediate offsets.
+    uint32_t va[2];
+#pragma unroll
+    for (int dm = 0; dm < 2; ++dm) va[dm] = (uint32_t)(uintptr_t)(L + voff[dm]);
+    auto pv_half_imm = [&](auto slot_c, auto hf_c, h8 (&pf)[2][2]) __attribute__((always_inline)) {
+        constexpr int S = decltype(slot_c)::value, HF = decltype(hf_c)::value;
+        constexpr int B0 = (S * SLOT + (HF * 2 + 0) * 16 * kD) * 2;
+        constexpr int B1 = (S * SLOT + (HF * 2 + 1) * 16 * kD) * 2;
+        s4_t r0[4], r1[4];
+        lds_read_tr16_issue4<B0>(va[0], va[1], r0);
+        lds_read_tr16_issue4<B1>(va[0], va[1], r1);
+        lds_wait_tied<4>(r0);
+        const h8 v00 = cat_h8(r0[0], r0[1]), v01 = cat_h8(r0[2], r0[3]);
+        o[0][0] = mfma32x32x16(v00, pf[0][0], o[0][0]);
+        o[1][0] = mfma32x32x16(v00, pf[1][0], o[1][0]);
+        o[0][1] = mfma32x32x16(v01, pf[0][0], o[0][1]);
+        o[1][1] = mfma32x32x16(v01, pf[1][0], o[1][1]);
+        lds_wait_tied<0>(r1);
+        const h8 v10 = cat_h8(r1[0], r1[1]), v11 = cat_h8(r1[2], r1[3]);
+        o[0][0] = mfma32x32x16(v10, pf[0][1], o[0][0]);
+        o[1][0] = mfma32x32x16(v10, pf[1][1], o[1][0]);
+        o[0][1] = mfma32x32x16(v11, pf[0][1], o[0][1]);
+        o[1][1] = mfma32x32x16(v11, pf[1][1], o[1][1]);
+    };
+    // slot_c: the ring slot as a compile-time constant, or -1 for a slot
+    // known only at run time (Ks).
+    auto block = [&](auto tail_c, auto slot_c, const lds_half_t* Ks, int key_base)
+                     __attribute__((always_inline)) {
+        constexpr int S = decltype(slot_c)::value;
         f16x sa[2], sb[2];
         h8 pa[2][2], pb[2][2];
         s_half(Ks, 0, sa);
         softmax_half(tail_c, key_base, sa, pa);
-        pv_half(Ks, 0, pa);
+        if constexpr (S >= 0)
+            pv_half_imm(slot_c, std::integral_constant<int, 0>{}, pa);
+        else
+            pv_half(Ks, 0, pa);
         s_half(Ks, 1, sb);
         softmax_half(tail_c, key_base + 32, sb, pb);
-        pv_half(Ks, 1, pb);
+        if constexpr (S >= 0)
+            pv_half_imm(slot_c, std::integral_constant<int, 1>{}, pb);
+        else
+            pv_half(Ks, 1, pb);
     };
+    using runtime_slot = std::integral_constant<int, -1>;
 
     const int nkb = (p.n_k + kKB - 1) / kKB;
     if constexpr (HPW == 1) {
         // 3-stage ring: blocks kb and kb + 1 in flight before block kb is used.
-        issue(0);
-        if (nkb > 1) issue(1);
-        for (int kb = 0; kb < nkb; ++kb) {
+        // The loop is unrolled by the ring's three slots, so every LDS
+        // address is a lane offset plus an immediate (a runtime slot index
+        // costs a VALU add per fragment address).
+        auto step = [&](auto slot_c, int kb) __attribute__((always_inline)) {
+            constexpr int S = decltype(slot_c)::value;
             if (kb + 1 < nkb)
                 asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA) : "memory");
             else
@@ -606,24 +676,31 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
             // Block kb has landed for every wave; slot (kb + 2) % 3 was last
             // read in iteration kb - 1, which every wave has finished.
             lds_barrier();
-            if (kb + 2 < nkb) issue(kb + 2);
+            if (kb + 2 < nkb) issue(L + ((S + 2) % NSLOT) * SLOT, kb + 2);
             // Full blocks only here; a partial last block is peeled below so
             // the masking code does not share this loop's registers.
-            if (wave_active && (kb + 1) * kKB <= p.n_k) block(std::false_type{}, slot_ptr(kb), kb * kKB);
+            if (wave_active && (kb + 1) * kKB <= p.n_k) block(std::false_type{}, slot_c, L + S * SLOT, kb * kKB);
+        };
+        issue(L, 0);
+        if (nkb > 1) issue(L + SLOT, 1);
+        for (int kb = 0; kb < nkb; kb += NSLOT) {
+            step(std::integral_constant<int, 0>{}, kb);
+            if (kb + 1 < nkb) step(std::integral_constant<int, 1>{}, kb + 1);
+            if (kb + 2 < nkb) step(std::integral_constant<int, 2>{}, kb + 2);
         }
         if (wave_active && nkb * kKB > p.n_k)
-            block(std::true_type{}, slot_ptr(nkb - 1), (nkb - 1) * kKB);
+            block(std::true_type{}, runtime_slot{}, slot_ptr(nkb - 1), (nkb - 1) * kKB);
     } else {
         // One block per wave, in the wave's own slot: the host selects this
         // variant only for sequences of at most 64 keys (launch_attention).
-        if (head_ok) issue(0);
+        if (head_ok) issue(slot_ptr(0), 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         lds_barrier();
         if (wave_active) {
             if (p.n_k < kKB)
-                block(std::true_type{}, slot_ptr(0), 0);
+                block(std::true_type{}, runtime_slot{}, slot_ptr(0), 0);
             else
-                block(std::false_type{}, slot_ptr(0), 0);
+                block(std::false_type{}, runtime_slot{}, slot_ptr(0), 0);
         }
     }
 
