@@ -992,6 +992,121 @@ int launch_attention(AttnParams& p, int64_t n_seq, int dtype, hipStream_t s) {
     return check_launch("attn_f32_kernel");
 }
 
+// ===========================================================================
+// Any head dim (msst_attention with D != 64)
+// ===========================================================================
+// The reference's scaled_dot_product_attention takes any head dim
+// (ops_attention.cu:522-599: scores materialized through cuBLAS, softmax,
+// then P.V).  D = 64, the Roformer head, runs the MFMA kernels above; any
+// other D up to 256 runs this kernel: fp32 arithmetic for both dtypes and
+// flash-style (online softmax over 32-key blocks staged in LDS as fp32), so
+// nothing of size N x Nk is allocated.  A workgroup takes 64 queries of
+// one (batch, head); thread (query ql, lane j < 4) holds dims j, j + 4, ...
+// of its query's Q (pre-scaled by scale log2 e) and of O.  The four lanes
+// of a query add their partial scores with two DPP quad permutes and then
+// run the same online softmax.  LDS rows are DP = 4 NC floats, zero-filled
+// past D, so the dot products need no per-dim predicate.
+constexpr int kGenKB = 32;
+
+__device__ __forceinline__ float quad_xor_sum(float x) {
+    // quad_perm [1,0,3,2] (lane ^ 1), then [2,3,0,1] (lane ^ 2).
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));
+    return x;
+}
+
+template <typename T, int NC>
+__global__ __launch_bounds__(256) void attn_generic_kernel(const T* __restrict__ q,
+                                                           const T* __restrict__ k,
+                                                           const T* __restrict__ v,
+                                                           T* __restrict__ out, int N, int Nk,
+                                                           int D, int qtiles, float scale_log2) {
+    constexpr int DP = 4 * NC;
+    __shared__ float Ks[kGenKB * DP], Vs[kGenKB * DP];
+    const int64_t bh = blockIdx.x / qtiles;
+    const int qt = (int)(blockIdx.x % qtiles);
+    const int tid = threadIdx.x, ql = tid >> 2, j = tid & 3;
+    const int qi = qt * 64 + ql;
+    const bool qok = qi < N;
+    const T* qrow = q + (bh * N + (qok ? qi : 0)) * D;
+    float qv[NC], ov[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int d = j + 4 * c;
+        qv[c] = (qok && d < D) ? (float)qrow[d] * scale_log2 : 0.0f;
+        ov[c] = 0.0f;
+    }
+    const T* kbase = k + bh * Nk * D;
+    const T* vbase = v + bh * Nk * D;
+    float m = -INFINITY, l = 0.0f;
+    for (int k0 = 0; k0 < Nk; k0 += kGenKB) {
+        const int nk = min(kGenKB, Nk - k0);
+        __syncthreads();  // every thread has finished reading the previous block
+        for (int e = tid; e < kGenKB * DP; e += 256) {
+            const int r = e / DP, d = e % DP;
+            const bool ok = r < nk && d < D;
+            const int64_t src = (int64_t)(k0 + r) * D + d;
+            Ks[e] = ok ? (float)kbase[src] : 0.0f;
+            Vs[e] = ok ? (float)vbase[src] : 0.0f;
+        }
+        __syncthreads();
+        float sc[kGenKB];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < kGenKB; ++r) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc = fmaf(qv[c], Ks[r * DP + j + 4 * c], acc);
+            acc = quad_xor_sum(acc);
+            sc[r] = r < nk ? acc : -INFINITY;
+            bm = fmaxf(bm, sc[r]);
+        }
+        const float m_new = fmaxf(m, bm);
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 for the first block
+        l *= alpha;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) ov[c] *= alpha;
+#pragma unroll
+        for (int r = 0; r < kGenKB; ++r) {
+            const float pr = __builtin_amdgcn_exp2f(sc[r] - m_new);
+            l += pr;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) ov[c] = fmaf(pr, Vs[r * DP + j + 4 * c], ov[c]);
+        }
+        m = m_new;
+    }
+    if (!qok) return;
+    T* orow = out + (bh * N + qi) * D;
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int d = j + 4 * c;
+        if (d < D) orow[d] = (T)(ov[c] * inv);
+    }
+}
+
+template <typename T, int NC>
+int launch_generic_nc(const void* q, const void* k, const void* v, void* out, int64_t BH, int N,
+                      int Nk, int D, int qtiles, float scale_log2, hipStream_t s) {
+    hipLaunchKernelGGL((attn_generic_kernel<T, NC>), dim3((unsigned)(BH * qtiles)), dim3(256), 0,
+                       s, static_cast<const T*>(q), static_cast<const T*>(k),
+                       static_cast<const T*>(v), static_cast<T*>(out), N, Nk, D, qtiles,
+                       scale_log2);
+    return check_launch("attn_generic_kernel");
+}
+
+template <typename T>
+int launch_generic(const void* q, const void* k, const void* v, void* out, int64_t BH, int N,
+                   int Nk, int D, int qtiles, float scale_log2, hipStream_t s) {
+    if (D <= 8) return launch_generic_nc<T, 2>(q, k, v, out, BH, N, Nk, D, qtiles, scale_log2, s);
+    if (D <= 16) return launch_generic_nc<T, 4>(q, k, v, out, BH, N, Nk, D, qtiles, scale_log2, s);
+    if (D <= 32) return launch_generic_nc<T, 8>(q, k, v, out, BH, N, Nk, D, qtiles, scale_log2, s);
+    if (D <= 64) return launch_generic_nc<T, 16>(q, k, v, out, BH, N, Nk, D, qtiles, scale_log2, s);
+    if (D <= 128)
+        return launch_generic_nc<T, 32>(q, k, v, out, BH, N, Nk, D, qtiles, scale_log2, s);
+    return launch_generic_nc<T, 64>(q, k, v, out, BH, N, Nk, D, qtiles, scale_log2, s);
+}
+
 bool fp32_lds_configured = false;
 
 int configure_f32_lds() {
@@ -1010,6 +1125,7 @@ int configure_f32_lds() {
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMaxGenericD = 4 * 64;
 
 }  // namespace
 }  // namespace msst
@@ -1021,17 +1137,29 @@ extern "C" int msst_attention(const void* q, const void* k, const void* v, void*
     MSST_REQUIRE(q && k && v && out, MSST_ERR_INVALID_ARG, "null tensor pointer");
     MSST_REQUIRE(is_dtype(dtype), MSST_ERR_INVALID_ARG, "bad dtype");
     MSST_REQUIRE(B >= 0 && H >= 0 && N >= 0 && Nk >= 0, MSST_ERR_INVALID_ARG, "bad shape");
-    MSST_REQUIRE(D == kD, MSST_ERR_UNSUPPORTED, "head dim must be 64");
+    MSST_REQUIRE(D >= 1 && D <= kMaxGenericD, MSST_ERR_UNSUPPORTED, "head dim must be in [1, 256]");
     MSST_REQUIRE(N < (1 << 30) && Nk < (1 << 30), MSST_ERR_UNSUPPORTED, "sequence too long");
-    MSST_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 16),
-                 MSST_ERR_ALIGNMENT, "q, k, v, out must be 16-byte aligned");
+    const size_t align = D == kD ? 16 : dtype_size(dtype);
+    MSST_REQUIRE(aligned(q, align) && aligned(k, align) && aligned(v, align) && aligned(out, align),
+                 MSST_ERR_ALIGNMENT,
+                 D == kD ? "q, k, v, out must be 16-byte aligned"
+                         : "q, k, v, out must be aligned to their element size");
     if (B * H == 0 || N == 0) return MSST_OK;
     MSST_REQUIRE(Nk > 0, MSST_ERR_INVALID_ARG, "no keys");
+    if (scale == 0.0f) scale = 1.0f / sqrtf((float)D);
+    if (D != kD) {
+        const int64_t qtiles = (N + 63) / 64;
+        MSST_REQUIRE(B * H <= 0x7fffffff / qtiles, MSST_ERR_UNSUPPORTED, "attention grid too large");
+        if (dtype == MSST_F32)
+            return launch_generic<float>(q, k, v, out, B * H, (int)N, (int)Nk, (int)D, (int)qtiles,
+                                         scale * kLog2e, as_stream(stream));
+        return launch_generic<half_t>(q, k, v, out, B * H, (int)N, (int)Nk, (int)D, (int)qtiles,
+                                      scale * kLog2e, as_stream(stream));
+    }
     if (dtype == MSST_F32) {
         int rc = configure_f32_lds();
         if (rc) return rc;
     }
-    if (scale == 0.0f) scale = 1.0f / sqrtf((float)D);
     AttnParams p{};
     p.q = q; p.k = k; p.v = v; p.out = out;
     p.ld_in = D; p.ld_out = D;

@@ -157,7 +157,11 @@ int msst_rope_qk(void* q, void* k, int dtype, const float* cos_t,
 
 /* out = softmax(scale * q.k^T) . v on contiguous [B,H,N,D] tensors
  * (k, v: [B,H,Nk,D]); dtype f32 (fp32 MFMA) or f16 (fp16 MFMA, fp32
- * softmax/accumulation).  scale == 0 means 1/sqrt(D).  D must be 64. */
+ * softmax/accumulation).  scale == 0 means 1/sqrt(D).  D = 64 (the
+ * Roformer head) runs the MFMA kernels and needs 16-byte aligned
+ * pointers; any other D in [1, 256] runs an fp32 flash kernel (no N x Nk
+ * buffer) and needs element-aligned pointers; D > 256 returns
+ * MSST_ERR_UNSUPPORTED. */
 int msst_attention(const void* q, const void* k, const void* v, void* out,
                    int dtype, int64_t B, int64_t H, int64_t N, int64_t Nk,
                    int64_t D, float scale, void* stream);

@@ -188,8 +188,25 @@ static void test_rope_attention() {
         check_close(std::string("scaled_dot_product_attention ") + (h ? "f16" : "f32"), o, r,
                     h ? 2e-2 : 1e-4);
     }
-    expect_throw("sdpa with head dim 32", [&] {
-        Tensor q = Tensor::zeros({1, 1, 4, 32});
+    // Head dims other than 64 (the reference takes any D): a ragged case
+    // through the generic kernel, and D > 256 refused.
+    for (DType dt : {DType::Float32, DType::Float16}) {
+        const bool h = dt == DType::Float16;
+        const int64_t b = 1, hh = 2, n = 70, nk = 45, d = 40;
+        auto q = randn(b * hh * n * d, 1.0f, 16), k = randn(b * hh * nk * d, 1.0f, 17),
+             v = randn(b * hh * nk * d, 1.0f, 18);
+        if (h) q = round16(q), k = round16(k), v = round16(v);
+        std::vector<float> r(b * hh * n * d);
+        orc_attention(q.data(), k.data(), v.data(), r.data(), b, hh, n, nk, d,
+                      1.0f / std::sqrt((float)d));
+        Tensor o = ops::scaled_dot_product_attention(dev(q, {b, hh, n, d}, dt),
+                                                     dev(k, {b, hh, nk, d}, dt),
+                                                     dev(v, {b, hh, nk, d}, dt));
+        check_close(std::string("scaled_dot_product_attention D=40 ") + (h ? "f16" : "f32"), o, r,
+                    h ? 2e-2 : 1e-4);
+    }
+    expect_throw("sdpa with head dim 300", [&] {
+        Tensor q = Tensor::zeros({1, 1, 4, 300});
         ops::scaled_dot_product_attention(q, q, q);
     });
     expect_throw("apply_rotary_emb on 3-D q", [&] {

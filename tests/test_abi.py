@@ -74,9 +74,15 @@ def test_linear_rejects_bad_arguments(msst):
 def test_attention_rejects_unsupported_head_dim(msst):
     lib = msst.lib()
     p = ctypes.c_void_p(0x1000)
-    rc = lib.msst_attention(p, p, p, p, 0, 1, 1, 8, 8, 32, 0.0, None)
-    assert rc == UNSUPPORTED and "64" in _last(msst)
+    for D in (0, 257, 300):
+        rc = lib.msst_attention(p, p, p, p, 0, 1, 1, 8, 8, D, 0.0, None)
+        assert rc == UNSUPPORTED and "256" in _last(msst)
+    # D = 64 (MFMA kernels) needs 16-byte alignment; other D element alignment.
     rc = lib.msst_attention(p, p, p, ctypes.c_void_p(0x1008), 0, 1, 1, 8, 8, 64, 0.0, None)
+    assert rc == ALIGN
+    rc = lib.msst_attention(p, p, p, ctypes.c_void_p(0x1002), 0, 1, 1, 8, 8, 32, 0.0, None)
+    assert rc == ALIGN
+    rc = lib.msst_attention(p, p, p, ctypes.c_void_p(0x1001), 1, 1, 1, 8, 8, 32, 0.0, None)
     assert rc == ALIGN
 
 

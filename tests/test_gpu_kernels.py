@@ -268,6 +268,26 @@ def test_attention(msst, oracle, cuda, B, H, N, Nk, dt):
     assert rel_err(host(y), r) < tol(dt)
 
 
+@pytest.mark.parametrize("D", [1, 6, 16, 32, 40, 80, 96, 128, 200, 256])
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+def test_attention_any_head_dim(msst, oracle, cuda, D, dt):
+    """Head dims other than 64 (the reference's scaled_dot_product_attention
+    takes any D): the generic fp32 flash kernel, ragged N and Nk (partial
+    query tile, partial last key block), two heads."""
+    B, H, N = 2, 2, 70
+    Nk = 45 if D % 2 else 97
+    rng = np.random.default_rng(D)
+    q = rng.standard_normal((B, H, N, D)).astype(np.float32)
+    k = rng.standard_normal((B, H, Nk, D)).astype(np.float32)
+    v = rng.standard_normal((B, H, Nk, D)).astype(np.float32)
+    if dt == "f16":
+        q, k, v = r16(q), r16(k), r16(v)
+    y = msst.attention(dev(q, tdt(dt)), dev(k, tdt(dt)), dev(v, tdt(dt)))
+    r = oracle.attention(q, k, v)
+    # fp32 arithmetic for both dtypes: the fp16 error is the output rounding.
+    assert rel_err(host(y), r) < (1e-5 if dt == "f32" else 1e-3)
+
+
 def _fused_reference(oracle, qkv, gates, cos_t, sin_t, B, F, T, H, axis):
     """Oracle path for one attention block on [B,F,T] token order."""
     D = 64
