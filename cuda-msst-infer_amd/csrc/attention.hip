@@ -457,17 +457,21 @@ __device__ __forceinline__ float pair_sum(float a) {
 constexpr float kRescaleLog2 = 8.0f;
 
 template <int HPW>
-__global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(AttnParams p) {
+constexpr int dma_nslot() { return HPW == 1 ? 3 : 4; }
+
+// One work item of attn_f16_dma_kernel.  QT: 32-query column blocks per wave
+// (2: 64 queries per wave; 1: the tail q-tile of a sequence, 16 queries per
+// wave, so its rows are spread over the workgroup's waves).
+template <int HPW, int QT>
+__device__ __forceinline__ void attn_dma_item(const AttnParams& p, int64_t sh, int qt_idx,
+                                              half_t* lds) {
     constexpr int WPH = 4 / HPW;
-    constexpr int NSLOT = HPW == 1 ? 3 : 4;
+    constexpr int NSLOT = dma_nslot<HPW>();
     constexpr int SLOT = 2 * kKB * kD;          // halves: K tile, then V tile
     constexpr int ROWS_W = HPW == 1 ? 16 : 64;  // block rows one wave DMAs
     constexpr int NDMA = 2 * ROWS_W / 8;        // DMA instructions per wave per block
-    __shared__ __attribute__((aligned(16))) half_t lds[NSLOT * SLOT];
-
-    int64_t sh;
-    int qt_idx;
-    if (!work_item(p, sh, qt_idx)) return;
+    constexpr int QROWS = QT == 2 ? 64 : 16;    // queries per wave
+    static_assert(QT == 2 || HPW == 1, "tail q-tiles are split only in the one-head form");
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -478,16 +482,17 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
     const int64_t seq = sh / head_groups;
     const int h = hg * HPW + head_local;
     const bool head_ok = h < p.H;  // always true for HPW = 1
-    const int q0 = (qt_idx * WPH + qsub) * 64;
+    const int q0 = QT == 2 ? (qt_idx * WPH + qsub) * 64 : qt_idx * WPH * 64 + w * QROWS;
+    const int q_end = min(q0 + QROWS, p.n_q);  // this wave's queries: [q0, q_end)
     const bool wave_active = head_ok && q0 < p.n_q;
 
     // ---- Q operand (B of S^T), held for the whole loop.
     const half_t* qb = reinterpret_cast<const half_t*>(p.q);
-    h8 qf[2][4];
+    h8 qf[QT][4];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int qi = q0 + qt * 32 + lrow;
-        const bool ok = wave_active && qi < p.n_q;
+        const bool ok = wave_active && qi < q_end;
         const half_t* row = qb + (ok ? tok_q(p, seq, qi) * p.ld_in + h * p.head_in : 0);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
@@ -535,33 +540,35 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
     for (int dm = 0; dm < 2; ++dm)
         voff[dm] = kKB * kD + vrow * kD + (((4 * dm + vch) ^ vsw) << 3) + vsub;
 
-    f16x o[2][2];
+    f16x o[QT][2];
+    float m_run[QT], l_run[QT];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b) o[a][b] = f16x{};
-    float m_run[2] = {-INFINITY, -INFINITY};
-    float l_run[2] = {0.0f, 0.0f};
+    for (int a = 0; a < QT; ++a) {
+        o[a][0] = f16x{};
+        o[a][1] = f16x{};
+        m_run[a] = -INFINITY;
+        l_run[a] = 0.0f;
+    }
     const float c = p.scale_log2;
     const float th = kRescaleLog2 / c;
     const h2 ones = h2{(half_t)1.0f, (half_t)1.0f};
 
     // S^T for the 32 keys of half hf: sh[qt] (keys hf*32 + 8 (v/4) + 4 lh + v%4).
-    auto s_half = [&](const lds_half_t* Ks, int hf, f16x (&shf)[2]) {
-        shf[0] = f16x{};
-        shf[1] = f16x{};
+    auto s_half = [&](const lds_half_t* Ks, int hf, f16x (&shf)[QT]) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) shf[qt] = f16x{};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             const h8 kf = *(const lds_h8_t*)(Ks + kofs[kk] + hf * 32 * kD);
-            shf[0] = mfma32x32x16(kf, qf[0][kk], shf[0]);
-            shf[1] = mfma32x32x16(kf, qf[1][kk], shf[1]);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) shf[qt] = mfma32x32x16(kf, qf[qt][kk], shf[qt]);
         }
     };
     // Online softmax of one half: P^T operands pf[qt][tp] (16-key substeps).
-    auto softmax_half = [&](auto tail_c, int key0, f16x (&shf)[2], h8 (&pf)[2][2]) {
+    auto softmax_half = [&](auto tail_c, int key0, f16x (&shf)[QT], h8 (&pf)[QT][2]) {
         constexpr bool TAIL = decltype(tail_c)::value;
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
+        for (int qt = 0; qt < QT; ++qt) {
             if constexpr (TAIL) {
                 // Register v holds key key0 + 4 lh + 8 (v / 4) + v % 4: one
                 // per-lane limit against immediates (no per-key registers).
@@ -601,7 +608,7 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
         }
     };
     // O^T += V^T . P^T over the two 16-key substeps of half hf.
-    auto pv_half = [&](const lds_half_t* Ks, int hf, h8 (&pf)[2][2]) {
+    auto pv_half = [&](const lds_half_t* Ks, int hf, h8 (&pf)[QT][2]) {
 #pragma unroll
         for (int tp = 0; tp < 2; ++tp)
 #pragma unroll
@@ -610,8 +617,8 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
                 const h4 lo = lds_read_tr16(vp);
                 const h4 hi = lds_read_tr16(vp + 8 * kD);
                 const h8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                o[0][dm] = mfma32x32x16(vf, pf[0][tp], o[0][dm]);
-                o[1][dm] = mfma32x32x16(vf, pf[1][tp], o[1][dm]);
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) o[qt][dm] = mfma32x32x16(vf, pf[qt][tp], o[qt][dm]);
             }
     };
     // The same with the slot S and half HF known at compile time: the V^T
@@ -619,7 +626,7 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
     uint32_t va[2];
 #pragma unroll
     for (int dm = 0; dm < 2; ++dm) va[dm] = (uint32_t)(uintptr_t)(L + voff[dm]);
-    auto pv_half_imm = [&](auto slot_c, auto hf_c, h8 (&pf)[2][2]) __attribute__((always_inline)) {
+    auto pv_half_imm = [&](auto slot_c, auto hf_c, h8 (&pf)[QT][2]) __attribute__((always_inline)) {
         constexpr int S = decltype(slot_c)::value, HF = decltype(hf_c)::value;
         constexpr int B0 = (S * SLOT + (HF * 2 + 0) * 16 * kD) * 2;
         constexpr int B1 = (S * SLOT + (HF * 2 + 1) * 16 * kD) * 2;
@@ -628,24 +635,24 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
         lds_read_tr16_issue4<B1>(va[0], va[1], r1);
         lds_wait_tied<4>(r0);
         const h8 v00 = cat_h8(r0[0], r0[1]), v01 = cat_h8(r0[2], r0[3]);
-        o[0][0] = mfma32x32x16(v00, pf[0][0], o[0][0]);
-        o[1][0] = mfma32x32x16(v00, pf[1][0], o[1][0]);
-        o[0][1] = mfma32x32x16(v01, pf[0][0], o[0][1]);
-        o[1][1] = mfma32x32x16(v01, pf[1][0], o[1][1]);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) o[qt][0] = mfma32x32x16(v00, pf[qt][0], o[qt][0]);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) o[qt][1] = mfma32x32x16(v01, pf[qt][0], o[qt][1]);
         lds_wait_tied<0>(r1);
         const h8 v10 = cat_h8(r1[0], r1[1]), v11 = cat_h8(r1[2], r1[3]);
-        o[0][0] = mfma32x32x16(v10, pf[0][1], o[0][0]);
-        o[1][0] = mfma32x32x16(v10, pf[1][1], o[1][0]);
-        o[0][1] = mfma32x32x16(v11, pf[0][1], o[0][1]);
-        o[1][1] = mfma32x32x16(v11, pf[1][1], o[1][1]);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) o[qt][0] = mfma32x32x16(v10, pf[qt][1], o[qt][0]);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) o[qt][1] = mfma32x32x16(v11, pf[qt][1], o[qt][1]);
     };
     // slot_c: the ring slot as a compile-time constant, or -1 for a slot
     // known only at run time (Ks).
     auto block = [&](auto tail_c, auto slot_c, const lds_half_t* Ks, int key_base)
                      __attribute__((always_inline)) {
         constexpr int S = decltype(slot_c)::value;
-        f16x sa[2], sb[2];
-        h8 pa[2][2], pb[2][2];
+        f16x sa[QT], sb[QT];
+        h8 pa[QT][2], pb[QT][2];
         s_half(Ks, 0, sa);
         softmax_half(tail_c, key_base, sa, pa);
         if constexpr (S >= 0)
@@ -707,10 +714,10 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
     if (!wave_active) return;
     half_t* ob = reinterpret_cast<half_t*>(p.out);
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int qi = q0 + qt * 32 + lrow;
         const float l_tot = pair_sum(l_run[qt]);
-        if (qi >= p.n_q) continue;
+        if (qi >= q_end) continue;
         const int64_t tok = tok_q(p, seq, qi);
         float scale = 1.0f / l_tot;
         if (p.gates) scale *= p.gates[tok * p.H + h];
@@ -726,6 +733,24 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
                 *reinterpret_cast<h4*>(orow + d) = val;
             }
     }
+}
+
+template <int HPW>
+__global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) half_t lds[dma_nslot<HPW>() * 2 * kKB * kD];
+    int64_t sh;
+    int qt_idx;
+    if (!work_item(p, sh, qt_idx)) return;
+    if constexpr (HPW == 1) {
+        // The tail q-tile of a sequence with at most 64 queries left would
+        // run one wave of four for the full key loop; its rows go 16 per wave
+        // instead (one 32-query column block each: half a wave's MFMA work).
+        if (qt_idx == p.qtiles - 1 && p.n_q - qt_idx * 256 <= 64) {
+            attn_dma_item<1, 1>(p, sh, qt_idx, lds);
+            return;
+        }
+    }
+    attn_dma_item<HPW, 2>(p, sh, qt_idx, lds);
 }
 
 // ===========================================================================
