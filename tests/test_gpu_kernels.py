@@ -251,7 +251,10 @@ def test_rope_table_device(msst, oracle, cuda):
 
 # --------------------------------------------------------------- attention
 ATTN = [(1, 1, 1, 1), (2, 3, 17, 19), (1, 2, 62, 62), (2, 8, 60, 60), (1, 3, 64, 64),
-        (1, 2, 65, 65), (1, 2, 129, 70), (2, 8, 801, 801), (1, 1, 300, 1000)]
+        (1, 2, 65, 65), (1, 2, 129, 70), (2, 8, 801, 801), (1, 1, 300, 1000),
+        # the last q-tile of a sequence split over the workgroup's waves: a tail of
+        # exactly 64 queries, of 1 query, and of 1 query with N != Nk
+        (1, 2, 832, 832), (1, 2, 769, 769), (2, 3, 257, 300)]
 
 
 @pytest.mark.parametrize("B,H,N,Nk", ATTN)
