@@ -1196,6 +1196,13 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
             //    in the stack on one box).
             const bool small = ((M + 255) / 256) * ((N + 255) / 256) < 256;
             const bool narrow_res = res != nullptr && K <= 512;
+            // N = 384 (MelBandRoformer's dim): whole-width 192 x 384 tiles, 12
+            // waves of 96 x 64, three per SIMD.  The bytes fetched per flop of
+            // a 256 x 256 tile (where 256 x 128 fetches 1.5 times as many), and
+            // M = 48060 makes 251 tiles: one round on 256 CUs.
+            if (act == MSST_ACT_NONE && N == 384 && !small)
+                return launch_f16_dma<192, 384, 32, 3, 1, 6, OutT>(xh, wh, bias, res, o, m, n, k, act,
+                                                                   s);
             if (act == MSST_ACT_NONE && (small || narrow_res) && N % 4 == 0)
                 return launch_f16_dma<128, 128, 32, 3, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act,
                                                                    s);
