@@ -1164,7 +1164,7 @@ extern "C" int msst_attention(const void* q, const void* k, const void* v, void*
     MSST_REQUIRE(B >= 0 && H >= 0 && N >= 0 && Nk >= 0, MSST_ERR_INVALID_ARG, "bad shape");
     MSST_REQUIRE(D >= 1 && D <= kMaxGenericD, MSST_ERR_UNSUPPORTED, "head dim must be in [1, 256]");
     MSST_REQUIRE(N < (1 << 30) && Nk < (1 << 30), MSST_ERR_UNSUPPORTED, "sequence too long");
-    const size_t align = D == kD ? 16 : dtype_size(dtype);
+    const size_t align = D == kD ? 16 : dtype_bytes(dtype);
     MSST_REQUIRE(aligned(q, align) && aligned(k, align) && aligned(v, align) && aligned(out, align),
                  MSST_ERR_ALIGNMENT,
                  D == kD ? "q, k, v, out must be 16-byte aligned"

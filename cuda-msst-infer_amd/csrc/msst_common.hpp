@@ -263,7 +263,6 @@ int set_error(int code, const std::string& msg);
 int check_launch(const char* what);
 
 inline bool is_dtype(int dt) { return dt == MSST_F32 || dt == MSST_F16; }
-inline size_t dtype_size(int dt) { return dt == MSST_F32 ? 4 : 2; }
 inline size_t dtype_bytes(int dt) { return dt == MSST_F16 ? 2 : 4; }
 inline bool aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) % a) == 0;
