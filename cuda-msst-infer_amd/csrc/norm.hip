@@ -261,8 +261,11 @@ __global__ __launch_bounds__(kThreads) void rms_norm_gate_h_kernel(
 template <typename XT, int NS, int GP>
 void launch_gate_h(const void* x, const float* gamma, float scale, void* out, const void* wg,
                    const float* bg, float* gates, int64_t rows, int D, int G, hipStream_t s) {
-    int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
-    if (blocks > 1024) blocks = 1024;
+    // At most 4096 waves, each with the same number of rows (a wave striding
+    // by the wave count would otherwise leave the last row-time to a few).
+    const int64_t per_wave = (rows + 4095) / 4096;
+    const int64_t nw = (rows + per_wave - 1) / per_wave;
+    const int64_t blocks = (nw + kRowsPerBlock - 1) / kRowsPerBlock;
     hipLaunchKernelGGL((rms_norm_gate_h_kernel<XT, NS, GP>), dim3((unsigned)blocks),
                        dim3(kThreads), 0, s, reinterpret_cast<const XT*>(x), gamma, scale,
                        reinterpret_cast<half_t*>(out), reinterpret_cast<const half_t*>(wg), bg,
