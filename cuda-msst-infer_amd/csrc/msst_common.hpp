@@ -47,21 +47,22 @@ __device__ __forceinline__ f16x mfma32x32x2f32(float a, float b, f16x c) {
 
 // ---------------------------------------------------------------------------
 // Epilogue activations.
-// GELU(v) = v Phi(v), Phi(v) = (1 + erf(v / sqrt 2)) / 2, with erf from
-// Abramowitz & Stegun, Handbook of Mathematical Functions (1964), formula
-// 7.1.26:
-//   1 - erf(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),
-//   t = 1 / (1 + p z), z >= 0,  |error| <= 1.5e-7.
-// With c = (1 - erf(|v| / sqrt 2)) / 2 = Phi(-|v|) (the polynomial's
-// coefficients halved, p folded with 1 / sqrt 2), v Phi(v) is v (1 - c) for
-// v >= 0 and v c for v < 0: both are v / 2 + |v| (1/2 - c), one FMA with
-// |v| as a free source modifier and no select, min or max (whose operands
-// the compiler would first canonicalise).  Fourteen VALU operations
-// (v_rcp_f32 and v_exp_f32 among them) against several times that for the
-// library erff, which dominated the FF1 epilogue.  Error: the approximation's
-// 0.75e-7 |v| plus the rounding of 1/2 - c (3e-8 |v|), far below the fp16
-// output rounding and the 1e-4 fp32 tolerance.  v = +inf gives +inf
-// (t = e = 0); v = -inf gives NaN, as v Phi(v) does.
+// GELU(v) = v Phi(v), Phi(v) = (1 + erf(v / sqrt 2)) / 2, the reference's
+// 0.5 v (1 + erff(v / sqrt 2)) (ops_fused.cu:21-24).  With a = |v| and
+// c = Phi(-a), v Phi(v) is v (1 - c) for v >= 0 and v c for v < 0: both are
+// v / 2 + a (1/2 - c), one FMA with |v| as a free source modifier instead of
+// a select on the sign.  c = 2^P(x), x = min(a, 5.6) (v_minimum_f32, which
+// does not canonicalise its operands as fminf would), P of degree 6: log2 Phi(-x) fitted minimax in
+// the absolute error of c on [0, 5.6] (a linear program on 3000 points,
+// gelu_fit.py beside this file regenerates the coefficients), |error of c|
+// <= 8.9e-8.  Past 5.6 the clamp keeps c = Phi(-5.6) = 1.1e-8, which rounds
+// away against 1/2.  Eleven VALU operations with one v_exp_f32, against
+// thirteen with v_exp_f32 and v_rcp_f32 for the rational erf of Abramowitz &
+// Stegun 7.1.26 (FF1 168 -> 162 us) and several times that for the library
+// erff.  Error, with fp32 evaluation and v_exp_f32 off by one ulp either
+// way: <= 2.4e-7 |v| over all finite v, far below the fp16 output rounding
+// and the 1e-4 fp32 tolerance.  v = +inf gives +inf, v = -inf NaN (as
+// 0.5 v (1 + erf) does), NaN stays NaN.
 // sigmoid(v) = 1 / (1 + 2^(-v log2 e)) with v_exp_f32 and v_rcp_f32 (each
 // about 1 ulp): relative error ~3e-7 in 4 VALU operations instead of the
 // library expf and an IEEE division; v -> -inf gives rcp(inf) = 0, v -> +inf
@@ -69,14 +70,15 @@ __device__ __forceinline__ f16x mfma32x32x2f32(float a, float b, f16x c) {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float gelu_erf(float v) {
     const float a = fabsf(v);
-    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752f, a, 1.0f));
-    float p = fmaf(t, 0.5f * 1.061405429f, 0.5f * -1.453152027f);
-    p = fmaf(t, p, 0.5f * 1.421413741f);
-    p = fmaf(t, p, 0.5f * -0.284496736f);
-    p = fmaf(t, p, 0.5f * 0.254829592f);
-    // exp(-v^2 / 2) = 2^(-v^2 log2(e) / 2); v_exp_f32 flushes to 0 far out.
-    const float e = __builtin_amdgcn_exp2f(v * (v * -0.72134752044448170f));
-    const float c = (p * t) * e;
+    // v_minimum_f32: no canonicalisation, and a NaN stays NaN.
+    const float x = __builtin_elementwise_minimum(a, 5.6f);
+    float p = fmaf(x, 1.984903428819962e-05f, -6.632566801272333e-04f);
+    p = fmaf(x, p, 7.766014896333218e-03f);
+    p = fmaf(x, p, -5.297756940126419e-02f);
+    p = fmaf(x, p, -4.590558707714081e-01f);
+    p = fmaf(x, p, -1.151121973991394f);
+    p = fmaf(x, p, -9.999997615814209e-01f);
+    const float c = __builtin_amdgcn_exp2f(p);
     return fmaf(a, 0.5f - c, 0.5f * v);
 }
 

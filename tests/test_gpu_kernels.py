@@ -106,10 +106,12 @@ def test_linear_small(msst, oracle, cuda, M, K, N, wd, xd, od, act):
 
 @pytest.mark.parametrize("wd", ["f16", "f32"])
 def test_gelu_error_bound(msst, cuda, wd):
-    """The epilogue GELU (Abramowitz & Stegun 7.1.26 erf, |error| <= 1.5e-7)
-    against float64 erf.  W = I makes the pre-activation exactly x, so the
-    measured error is the activation's own: <= 5e-7 |x| (approximation plus
-    fp32 evaluation) for fp32 output, plus half an fp16 ulp for fp16 output."""
+    """The epilogue GELU (v/2 + |v| (1/2 - 2^P(min(|v|, 5.6))), P a degree-6
+    minimax fit of log2 Phi(-a)) against float64 erf.  W = I makes the
+    pre-activation exactly x, so the measured error is the activation's own:
+    <= 2.4e-7 |x| by the float32 analysis of the fit (approximation, fp32
+    evaluation, v_exp_f32 off by one ulp), checked here at 3.5e-7 |x| for fp32
+    output, plus half an fp16 ulp for fp16 output."""
     from scipy.special import erf
     n = 64
     x = np.linspace(-12.0, 12.0, 4096 * n, dtype=np.float64)
@@ -122,7 +124,7 @@ def test_gelu_error_bound(msst, cuda, wd):
     exact = 0.5 * x.astype(np.float64) * (1.0 + erf(x.astype(np.float64) / np.sqrt(2.0)))
     y32 = host(msst.linear(dev(x, tdt(wd)), dev(w, tdt(wd)), None, "gelu",
                            out_dtype=torch.float32)).astype(np.float64)
-    bound = 5e-7 * np.abs(x) + 1e-30
+    bound = 3.5e-7 * np.abs(x) + 1e-30
     assert np.all(np.abs(y32 - exact) <= bound), float(np.max(np.abs(y32 - exact) / bound))
     y16 = host(msst.linear(dev(x, tdt(wd)), dev(w, tdt(wd)), None, "gelu",
                            out_dtype=torch.float16)).astype(np.float64)
