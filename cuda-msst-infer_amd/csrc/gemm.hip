@@ -1033,8 +1033,11 @@ int launch_pp(const half_t* x, const half_t* w, const float* bias, const OutT* r
                                                                    act, s, *rope);
         else
             return set_error(MSST_ERR_UNSUPPORTED, "RoPE epilogue needs fp16 output");
+    } else if (act == MSST_ACT_GELU && !res) {
+        launch_pp_epi<BK, NSTG, kEpiPlain, MSST_ACT_GELU, OutT>(x, w, bias, res, out, M, N, K, act,
+                                                                s, EpiRope{});
     } else if (act != MSST_ACT_NONE) {
-        return set_error(MSST_ERR_UNSUPPORTED, "ping-pong GEMM takes no activation");
+        return set_error(MSST_ERR_UNSUPPORTED, "ping-pong GEMM takes no activation but GELU");
     } else if (res) {
         launch_pp_epi<BK, NSTG, kEpiRes, MSST_ACT_NONE, OutT>(x, w, bias, res, out, M, N, K, act,
                                                               s, EpiRope{});
@@ -1199,14 +1202,28 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
             // N = 384 (MelBandRoformer's dim): whole-width 192 x 384 tiles, 12
             // waves of 96 x 64, three per SIMD.  The bytes fetched per flop of
             // a 256 x 256 tile (where 256 x 128 fetches 1.5 times as many), and
-            // M = 48060 makes 251 tiles: one round on 256 CUs.
-            if (act == MSST_ACT_NONE && N == 384 && !small)
+            // M = 48060 makes 251 tiles: one round on 256 CUs.  At one tile per
+            // CU a short last round runs alone (K = 1536 with residual: 259
+            // tiles 118 us against 77 us for 256), and with K < 1024 the
+            // epilogue outweighs the loop once a CU takes several tiles
+            // (K = 384, M = 192240: 186 against 160 us for 128 x 128 x 3).  So
+            // K >= 1024 takes them when the last round is empty or holds at
+            // least 64 tiles, smaller K only within one round.
+            const int64_t t384 = ((int64_t)M + 191) / 192;
+            const bool fit384 = K >= 1024 ? (t384 % 256 == 0 || t384 % 256 >= 64) : t384 <= 256;
+            if (act == MSST_ACT_NONE && N == 384 && !small && fit384)
                 return launch_f16_dma<192, 384, 32, 3, 1, 6, OutT>(xh, wh, bias, res, o, m, n, k, act,
                                                                    s);
             if (act == MSST_ACT_NONE && (small || narrow_res) && N % 4 == 0)
                 return launch_f16_dma<128, 128, 32, 3, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act,
                                                                    s);
             if (act == MSST_ACT_NONE && N % 256 == 0 && (!res || std::is_same<OutT, float>::value))
+                return launch_pp<32, 3, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
+            // GELU (the feed-forward's first linear) on the ping-pong tiles as
+            // well: with the 11-operation GELU the epilogue no longer needs
+            // other workgroups' main loops to hide it (FF1 170 -> 163.5 us,
+            // batch of 4 691 -> 638 us, MelBandRoformer 109 -> 105 us).
+            if (act == MSST_ACT_GELU && !res && !small && N % 256 == 0)
                 return launch_pp<32, 3, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
             if (act != MSST_ACT_NONE && N % 4 == 0)
                 return launch_f16_dma<128, 128, 32, 3, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act,

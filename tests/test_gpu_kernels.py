@@ -134,11 +134,14 @@ def test_gelu_error_bound(msst, cuda, wd):
 
 
 # Launches past one round of workgroups on 256 CUs (one 256 x 256 tile per
-# CU for N = 512, two 256 x 128 tiles for N = 384), with a partly filled
-# last round: in-place residual, bit-identical repeats, and a smaller launch
-# right after.  Reference: float32 BLAS on the same fp16-exact operands.
+# CU for N = 512; for N = 384 whole-width 192 x 384 tiles where the round
+# count allows, 256 x 128 or 128 x 128 tiles where it does not: 49662 rows
+# make 259 tiles of 192, 96120 rows two rounds at K = 384), with a partly
+# filled last round: in-place residual, bit-identical repeats, and a smaller
+# launch right after.  Reference: float32 BLAS on the same fp16-exact
+# operands.
 LARGE_SHAPES = [(40000, 512, 512), (40000, 2048, 512), (49662, 2048, 512), (48060, 1536, 384),
-             (48060, 384, 384)]
+             (48060, 384, 384), (49662, 1536, 384), (96120, 384, 384)]
 
 
 def _large_case(M, K, N, seed):
@@ -168,7 +171,7 @@ def test_linear_large_residual(msst, cuda, M, K, N):
     assert rel_err(host(xr2), ref[:M2]) < TOL_F32
 
 
-@pytest.mark.parametrize("M,K,N", [(40000, 512, 512), (48060, 1536, 384)])
+@pytest.mark.parametrize("M,K,N", [(40000, 512, 512), (48060, 1536, 384), (49662, 1536, 384)])
 def test_linear_large_plain_f16(msst, cuda, M, K, N):
     x, w, b, _ = _large_case(M, K, N, 7 * M + K)
     ref = x @ w.T + b
