@@ -1033,11 +1033,8 @@ int launch_pp(const half_t* x, const half_t* w, const float* bias, const OutT* r
                                                                    act, s, *rope);
         else
             return set_error(MSST_ERR_UNSUPPORTED, "RoPE epilogue needs fp16 output");
-    } else if (act == MSST_ACT_GELU && !res) {
-        launch_pp_epi<BK, NSTG, kEpiPlain, MSST_ACT_GELU, OutT>(x, w, bias, res, out, M, N, K, act,
-                                                                s, EpiRope{});
     } else if (act != MSST_ACT_NONE) {
-        return set_error(MSST_ERR_UNSUPPORTED, "ping-pong GEMM takes no activation but GELU");
+        return set_error(MSST_ERR_UNSUPPORTED, "ping-pong GEMM takes no activation");
     } else if (res) {
         launch_pp_epi<BK, NSTG, kEpiRes, MSST_ACT_NONE, OutT>(x, w, bias, res, out, M, N, K, act,
                                                               s, EpiRope{});
@@ -1218,12 +1215,6 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
                 return launch_f16_dma<128, 128, 32, 3, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act,
                                                                    s);
             if (act == MSST_ACT_NONE && N % 256 == 0 && (!res || std::is_same<OutT, float>::value))
-                return launch_pp<32, 3, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
-            // GELU (the feed-forward's first linear) on the ping-pong tiles as
-            // well: with the 11-operation GELU the epilogue no longer needs
-            // other workgroups' main loops to hide it (FF1 170 -> 163.5 us,
-            // batch of 4 691 -> 638 us, MelBandRoformer 109 -> 105 us).
-            if (act == MSST_ACT_GELU && !res && !small && N % 256 == 0)
                 return launch_pp<32, 3, OutT>(xh, wh, bias, res, o, m, n, k, act, s);
             if (act != MSST_ACT_NONE && N % 4 == 0)
                 return launch_f16_dma<128, 128, 32, 3, 3, 2, OutT>(xh, wh, bias, res, o, m, n, k, act,
