@@ -1201,13 +1201,16 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
             // a 256 x 256 tile (where 256 x 128 fetches 1.5 times as many), and
             // M = 48060 makes 251 tiles: one round on 256 CUs.  At one tile per
             // CU a short last round runs alone (K = 1536 with residual: 259
-            // tiles 118 us against 77 us for 256), and with K < 1024 the
-            // epilogue outweighs the loop once a CU takes several tiles
-            // (K = 384, M = 192240: 186 against 160 us for 128 x 128 x 3).  So
-            // K >= 1024 takes them when the last round is empty or holds at
-            // least 64 tiles, smaller K only within one round.
+            // tiles 118 us against 77 us for 256 tiles; 93 us on 256 x 128
+            // tiles), so they are taken when the last round is empty or holds
+            // at least 64 tiles.  The rule ignores K, although with K = 384 the
+            // 128 x 128 x 3 tiles are faster past one round (M = 192240: 160
+            // against 186 us): a batch of MelBandRoformer chunks (M = 4 x
+            // 48060) then takes the tiles of one chunk and computes the same
+            // bits (these tiles start their accumulators from the residual,
+            // the others add it in the epilogue).
             const int64_t t384 = ((int64_t)M + 191) / 192;
-            const bool fit384 = K >= 1024 ? (t384 % 256 == 0 || t384 % 256 >= 64) : t384 <= 256;
+            const bool fit384 = t384 % 256 == 0 || t384 % 256 >= 64;
             if (act == MSST_ACT_NONE && N == 384 && !small && fit384)
                 return launch_f16_dma<192, 384, 32, 3, 1, 6, OutT>(xh, wh, bias, res, o, m, n, k, act,
                                                                    s);

@@ -136,7 +136,7 @@ def test_gelu_error_bound(msst, cuda, wd):
 # Launches past one round of workgroups on 256 CUs (one 256 x 256 tile per
 # CU for N = 512; for N = 384 whole-width 192 x 384 tiles where the round
 # count allows, 256 x 128 or 128 x 128 tiles where it does not: 49662 rows
-# make 259 tiles of 192, 96120 rows two rounds at K = 384), with a partly
+# make 259 tiles of 192, 96120 rows 501), with a partly
 # filled last round: in-place residual, bit-identical repeats, and a smaller
 # launch right after.  Reference: float32 BLAS on the same fp16-exact
 # operands.
