@@ -1179,10 +1179,10 @@ int dispatch(const void* x, int x_dtype, const void* w, int w_dtype, const float
             // L2 -> LDS bytes per flop, run by the ping-pong kernel (6-8 %
             // faster than gemm_f16_dma_kernel on the same tiles, with
             // bit-identical results; fp16 residuals keep the latter, whose
-            // epilogue residual fits the register budget).  N = 128 (mod 256) (MelBandRoformer's
-            // dim 384) takes 256 x 128 tiles at two workgroups per CU instead
-            // of padding a quarter of the 256-wide tiles (out-proj / FF2
-            // 9-10 % faster).
+            // epilogue residual fits the register budget).  N = 128 (mod 256)
+            // takes 256 x 128 tiles at two workgroups per CU instead of padding
+            // a quarter of the 256-wide tiles (MelBandRoformer out-proj / FF2
+            // 9-10 % faster), unless N = 384 takes the 192 x 384 tiles below.
             // (The activation kernels start their accumulators from 16-byte
             // bias loads, which need N % 4 == 0; other N take the
             // register-staged kernel below.)
