@@ -94,7 +94,7 @@ extern "C" {
 
 /* Epilogue activations (ops_fused.cu:21-32). */
 #define MSST_ACT_NONE 0
-#define MSST_ACT_GELU 1    /* exact erf GELU */
+#define MSST_ACT_GELU 1    /* erf GELU, v Phi(v) (not the tanh form) */
 #define MSST_ACT_SIGMOID 2
 #define MSST_ACT_SILU 3
 
