@@ -13,8 +13,8 @@ Prints ONE JSON line:
   value          ms per 8 s chunk (lower is better), inputs resident in HBM
   gemm_tflops    the stack's MFMA GEMMs replayed alone (same shapes, same
                  epilogues, same stream) -> TFLOP/s and fraction of peak
-  roofline       dominant kernel = gemm_f16_dma_kernel (128x128 tiles, 3
-                 workgroups per CU, bias+GELU epilogue) on the FF1 shape
+  roofline       dominant kernel = gemm_pp_kernel (256x256 ping-pong tiles,
+                 8 waves, bias+GELU epilogue, nt stores) on the FF1 shape
                  (M=49662, K=512, N=2048, bias+GELU, fp16 out), HIP-event
                  timed over 50 launches on the stream it runs on; traffic =
                  HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE
@@ -625,7 +625,7 @@ def main():
         "gemm_frac_of_peak": round(gemm_tflops / PEAK_F16_TFLOPS, 4),
         "stack_tflops": round((gemm_flops + attn_flops_chunk(B)) / (ms_per_step * 1e-3) / 1e12, 1),
         "roofline": {
-            "kernel": f"gemm_f16_dma_kernel<128,128,32,3,3,2,plain,GELU,half> FF1 M={M} "
+            "kernel": f"gemm_pp_kernel<32,3,plain,GELU,half> FF1 M={M} "
                       "K=512 N=2048 bias+GELU fp16 out",
             "bound": "mfma",
             "achieved": round(ff1_tflops, 1),
