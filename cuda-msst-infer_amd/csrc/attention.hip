@@ -60,7 +60,7 @@ struct AttnParams {
     int64_t k_outer, k_inner, k_pos;
     int n_q, n_k;               // queries / keys per sequence
     int H;
-    int qtiles;                 // 64*waves_per_head-query tiles per (seq, head)
+    int qtiles;                 // q-tiles per (seq, head): waves_per_head x 64 queries (x 32: fp32, one head)
     int64_t total_items;        // workgroup work items
     int per_xcd;                // work items per XCD (see work_item)
     int short_last;             // most waves of a pair's last q-tile are idle
@@ -756,8 +756,8 @@ __global__ __launch_bounds__(256, HPW == 1 ? 3 : 2) void attn_f16_dma_kernel(Att
 // ===========================================================================
 // fp32
 // ===========================================================================
-template <int HPW>
-__global__ __launch_bounds__(256) void attn_f32_kernel(AttnParams p) {
+template <int HPW, int QT>
+__global__ __launch_bounds__(256, QT == 1 ? 2 : 1) void attn_f32_kernel(AttnParams p) {
     constexpr int WPH = 4 / HPW;
     constexpr int SLOT = 2 * kKB * kD;   // K block + V block (floats)
     constexpr int GROUP = 256 / HPW;
@@ -776,7 +776,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnParams p) {
     const int64_t seq = sh / head_groups;
     const int h = hg * HPW + head_local;
     const bool head_ok = h < p.H;
-    const int q0 = (qt_idx * WPH + qsub) * 64;
+    const int q0 = (qt_idx * WPH + qsub) * 32 * QT;
     const bool wave_active = head_ok && q0 < p.n_q;
 
     const float* qb = reinterpret_cast<const float*>(p.q);
@@ -784,9 +784,9 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnParams p) {
     const float* vbp = reinterpret_cast<const float*>(p.v);
 
     // Q operand: lane (query, half h) holds Q[q][32h .. 32h+31].
-    float qf[2][32];
+    float qf[QT][32];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int qi = q0 + qt * 32 + lrow;
         const bool ok = wave_active && qi < p.n_q;
         const float* row = qb + (ok ? tok_q(p, seq, qi) * p.ld_in + h * p.head_in : 0);
@@ -852,13 +852,17 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnParams p) {
         }
     };
 
-    f16x o[2][2];
+    f16x o[QT][2];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < QT; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b) o[a][b] = f16x{};
-    float m_run[2] = {-INFINITY, -INFINITY};
-    float l_run[2] = {0.0f, 0.0f};
+    float m_run[QT], l_run[QT];
+#pragma unroll
+    for (int a = 0; a < QT; ++a) {
+        m_run[a] = -INFINITY;
+        l_run[a] = 0.0f;
+    }
 
     const int nkb = (p.n_k + kKB - 1) / kKB;
     load_block(0);
@@ -871,27 +875,27 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnParams p) {
         if (wave_active) {
             const float* Ks = lds_f + slot * SLOT;
             const float* Vs = Ks + kKB * kD;
-            f16x s[2][2];
+            f16x s[2][QT];
 #pragma unroll
             for (int k2 = 0; k2 < 2; ++k2) {
-                s[k2][0] = f16x{};
-                s[k2][1] = f16x{};
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) s[k2][qt] = f16x{};
                 const int kr = k2 * 32 + lrow;
 #pragma unroll
                 for (int c = 0; c < 8; ++c) {
                     const int cc = 8 * lh + c;  // K dims 32h + 4c .. +3
                     f4 kf = *reinterpret_cast<const f4*>(Ks + kr * kD + ((cc ^ (kr & 15)) << 2));
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        s[k2][0] = mfma32x32x2f32(kf[e], qf[0][4 * c + e], s[k2][0]);
-                        s[k2][1] = mfma32x32x2f32(kf[e], qf[1][4 * c + e], s[k2][1]);
-                    }
+                    for (int e = 0; e < 4; ++e)
+#pragma unroll
+                        for (int qt = 0; qt < QT; ++qt)
+                            s[k2][qt] = mfma32x32x2f32(kf[e], qf[qt][4 * c + e], s[k2][qt]);
                 }
             }
             const int key_base = kb * kKB;
             const bool tail = key_base + kKB > p.n_k;
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+            for (int qt = 0; qt < QT; ++qt) {
                 float mx = -INFINITY;
 #pragma unroll
                 for (int k2 = 0; k2 < 2; ++k2)
@@ -934,8 +938,9 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnParams p) {
 #pragma unroll
                     for (int dm = 0; dm < 2; ++dm) {
                         const float vf = Vs[key * kD + dm * 32 + lrow];
-                        o[0][dm] = mfma32x32x2f32(vf, s[k2][0][v], o[0][dm]);
-                        o[1][dm] = mfma32x32x2f32(vf, s[k2][1][v], o[1][dm]);
+#pragma unroll
+                        for (int qt = 0; qt < QT; ++qt)
+                            o[qt][dm] = mfma32x32x2f32(vf, s[k2][qt][v], o[qt][dm]);
                     }
                 }
         }
@@ -946,7 +951,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(AttnParams p) {
     if (!wave_active) return;
     float* ob = reinterpret_cast<float*>(p.out);
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
         const int qi = q0 + qt * 32 + lrow;
         const float l_tot = l_run[qt] + __shfl_xor(l_run[qt], 32, 64);
         if (qi >= p.n_q) continue;
@@ -979,13 +984,16 @@ bool dma_fits(const AttnParams& p) {
 int launch_attention(AttnParams& p, int64_t n_seq, int dtype, hipStream_t s) {
     const int hpw = p.n_q <= 64 && p.n_k <= 64 ? 4 : 1;
     const int wph = 4 / hpw;
-    p.qtiles = (p.n_q + 64 * wph - 1) / (64 * wph);
+    // Queries per wave: 64, or 32 for the fp32 one-head kernel (QT = 1: half
+    // the Q / O / S registers, so two workgroups share a CU).
+    const int qw = dtype == MSST_F32 && hpw == 1 ? 32 : 64;
+    p.qtiles = (p.n_q + qw * wph - 1) / (qw * wph);
     const int64_t head_groups = (p.H + hpw - 1) / hpw;
     p.total_items = n_seq * head_groups * p.qtiles;
-    // A q-tile covers 64 * wph queries (64 per wave); the last one is
-    // reordered when at least half of its waves are idle (with fewer, the
-    // q-tiles of a pair running together in one L2 is worth more).
-    p.short_last = p.qtiles * 64 * wph - p.n_q >= 32 * wph ? 1 : 0;
+    // A q-tile covers qw * wph queries; the last one is reordered when at
+    // least half of its waves are idle (with fewer, the q-tiles of a pair
+    // running together in one L2 is worth more).
+    p.short_last = p.qtiles * qw * wph - p.n_q >= qw / 2 * wph ? 1 : 0;
     // Grid: 8 XCDs x work items per XCD (whole pairs per XCD when the last
     // q-tiles are reordered, see work_item).
     const int64_t per_xcd = p.short_last ? (n_seq * head_groups + 7) / 8 * p.qtiles
@@ -1009,10 +1017,10 @@ int launch_attention(AttnParams& p, int64_t n_seq, int dtype, hipStream_t s) {
     }
     if (hpw == 4) {
         const size_t lds = 4 * 2 * kKB * kD * sizeof(float);
-        hipLaunchKernelGGL(attn_f32_kernel<4>, dim3((unsigned)grid), dim3(256), lds, s, p);
+        hipLaunchKernelGGL((attn_f32_kernel<4, 2>), dim3((unsigned)grid), dim3(256), lds, s, p);
     } else {
         const size_t lds = 2 * 2 * kKB * kD * sizeof(float);
-        hipLaunchKernelGGL(attn_f32_kernel<1>, dim3((unsigned)grid), dim3(256), lds, s, p);
+        hipLaunchKernelGGL((attn_f32_kernel<1, 1>), dim3((unsigned)grid), dim3(256), lds, s, p);
     }
     return check_launch("attn_f32_kernel");
 }
@@ -1137,10 +1145,10 @@ bool fp32_lds_configured = false;
 int configure_f32_lds() {
     if (fp32_lds_configured) return MSST_OK;
     // 128 KB of dynamic LDS for the 4-head fp32 variant (gfx950 has 160 KB).
-    hipError_t e1 = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_f32_kernel<4>),
+    hipError_t e1 = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_f32_kernel<4, 2>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize,
                                         4 * 2 * kKB * kD * (int)sizeof(float));
-    hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_f32_kernel<1>),
+    hipError_t e2 = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_f32_kernel<1, 1>),
                                         hipFuncAttributeMaxDynamicSharedMemorySize,
                                         2 * 2 * kKB * kD * (int)sizeof(float));
     if (e1 != hipSuccess || e2 != hipSuccess)
