@@ -9,7 +9,9 @@
 // Kernels
 //   gemm_f16_kernel   f16 W (x f16 or f32, converted as it is staged):
 //                     v_mfma_f32_32x32x16_f16, fp32 accumulation.
-//   gemm_f32_kernel   f32 W: v_mfma_f32_32x32x2_f32 (true fp32, no TF32).
+//   gemm_f32_dma_kernel / gemm_f32_kernel
+//                     f32 W: v_mfma_f32_32x32x2_f32 (true fp32, no TF32); f32 x
+//                     with K % 32 == 0 through LDS DMA, otherwise staged.
 //   gemm_skinny       N <= 16 (the per-head gate projection): HBM-bound
 //                     row dot products, one wave per row.
 //   gemm_generic      any other shape (K not a multiple of the vector width).
@@ -302,6 +304,118 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
         if (kt + 1 < KT) store_tile(cur ^ 1);
         __syncthreads();
     }
+
+    constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
+    constexpr int kIP = pick_ip<MI, WN, kRegion>();
+    static_assert(kIP * 32 * WN <= kRegion, "epilogue staging does not fit in LDS");
+    store_tile_lds<MI, NI, kIP, RES ? kEpiRes : kEpiPlain, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+                                      lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act, residual,
+                                      out, vec != 0);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 x and W through LDS DMA (K % 32 == 0, 16-byte aligned rows, each
+// operand under 2 GiB): the tile, fragment reads and MFMA order of
+// gemm_f32_kernel (so the same results), without staging every k-tile
+// through VGPRs and ds_write.  A buffer_load_dwordx4 ... lds writes 8 LDS
+// rows of 128 bytes; lane l fetches source chunk (l & 7) ^ (row & 7), which
+// lands at chunk position l & 7: the XOR swizzle the fragment reads expect.
+// Rows past M / N are clamped to the last valid row (their results are
+// never stored).  Two stages: the DMA of k-tile t + 1 is issued right after
+// the barrier that opens k-tile t, one k-tile of MFMAs ahead of its use.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, bool RES, typename OutT>
+__global__ __launch_bounds__(kThreads) void gemm_f32_dma_kernel(
+    const float* __restrict__ A, const float* __restrict__ W, const float* __restrict__ bias,
+    const OutT* residual, OutT* out, int M, int N, int K, int act, int tiles_n, int per_xcd,
+    int vec) {
+    constexpr int BK = 32;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int MI = WM / 32, NI = WN / 32;
+    constexpr int RPI = 8;                    // LDS rows per DMA instruction
+    constexpr int NWAVE = kThreads / 64;
+    constexpr int A_INST = BM / RPI / NWAVE;  // per wave and k-tile
+    constexpr int B_INST = BN / RPI / NWAVE;
+    static_assert(A_INST * RPI * NWAVE == BM && B_INST * RPI * NWAVE == BN, "DMA split");
+
+    __shared__ __attribute__((aligned(16))) float lds[2][(BM + BN) * BK];
+
+    int tm, tn;
+    tile_coords(tiles_n, per_xcd, tm, tn, ((M + BM - 1) / BM) * tiles_n);
+    if (tm < 0) return;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wid >> 1, wn = wid & 1;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int sub = lane >> 3, pch = lane & 7;
+
+    const int a_bytes = M * K * 4, b_bytes = N * K * 4;  // < 2^31 (checked on the host)
+    uint32_t aoff[A_INST], boff[B_INST];
+#pragma unroll
+    for (int i = 0; i < A_INST; ++i) {
+        const int rl = (wid * A_INST + i) * RPI + sub;
+        aoff[i] = (uint32_t)(min(m0 + rl, M - 1) * K + ((pch ^ (rl & 7)) << 2)) * 4u;
+    }
+#pragma unroll
+    for (int i = 0; i < B_INST; ++i) {
+        const int rl = (wid * B_INST + i) * RPI + sub;
+        boff[i] = (uint32_t)(min(n0 + rl, N - 1) * K + ((pch ^ (rl & 7)) << 2)) * 4u;
+    }
+    auto issue = [&](int kt, int buf) {
+        const uint32_t kb = (uint32_t)(kt * BK) * 4u;
+        half_t* base = reinterpret_cast<half_t*>(&lds[buf][0]);  // 1 KB = 512 halves per DMA
+#pragma unroll
+        for (int i = 0; i < A_INST; ++i) dma16(A, a_bytes, base + (wid * A_INST + i) * 512, aoff[i] + kb);
+#pragma unroll
+        for (int i = 0; i < B_INST; ++i)
+            dma16(W, b_bytes, base + BM * BK * 2 + (wid * B_INST + i) * 512, boff[i] + kb);
+    };
+
+    f16x acc[MI][NI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NI; ++j) acc[i][j] = f16x{};
+
+    const int KT = K / BK;
+    issue(0, 0);
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        // k-tile kt has landed for this wave; after the barrier, for every
+        // wave, and every wave has finished reading buffer cur ^ 1 (k-tile
+        // kt - 1), which the next DMA overwrites.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        lds_barrier();
+        if (kt + 1 < KT) issue(kt + 1, cur ^ 1);
+        const float* As = lds[cur];
+        const float* Bs = lds[cur] + BM * BK;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int c = lhalf * 4 + t;
+            f4 af[MI], bf[NI];
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                int r = wm * WM + i * 32 + lrow;
+                af[i] = *reinterpret_cast<const f4*>(As + r * BK + ((c ^ (r & 7)) << 2));
+            }
+#pragma unroll
+            for (int j = 0; j < NI; ++j) {
+                int r = wn * WN + j * 32 + lrow;
+                bf[j] = *reinterpret_cast<const f4*>(Bs + r * BK + ((c ^ (r & 7)) << 2));
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NI; ++j)
+                        acc[i][j] = mfma32x32x2f32(af[i][s], bf[j][s], acc[i][j]);
+        }
+    }
+    lds_barrier();  // every wave is done with the last k-tile before the epilogue reuses LDS
 
     constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
     constexpr int kIP = pick_ip<MI, WN, kRegion>();
@@ -1102,6 +1216,17 @@ int launch_f32(const void* x, bool x_f16, const float* w, const float* bias,
     int per_xcd;
     int grid = num_xcd_slots((int64_t)tiles_m * tiles_n, per_xcd);
     const int vec = vec_flag(res, out, N);
+    if (!x_f16 && K % 32 == 0 && aligned(x, 16) && aligned(w, 16) &&
+        (int64_t)M * K * 4 < ((int64_t)1 << 31) && (int64_t)N * K * 4 < ((int64_t)1 << 31)) {
+        const float* xf = reinterpret_cast<const float*>(x);
+        if (res)
+            hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN, true, OutT>), dim3(grid), dim3(kThreads),
+                               0, s, xf, w, bias, res, out, M, N, K, act, tiles_n, per_xcd, vec);
+        else
+            hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN, false, OutT>), dim3(grid), dim3(kThreads),
+                               0, s, xf, w, bias, res, out, M, N, K, act, tiles_n, per_xcd, vec);
+        return check_launch("gemm_f32_dma_kernel");
+    }
 #define MSST_L32(AH, RS)                                                                        \
     hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, AH, RS, OutT>), dim3(grid), dim3(kThreads), 0, s, \
                        x, w, bias, res, out, M, N, K, act, tiles_n, per_xcd, vec)
