@@ -315,24 +315,30 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
 
 // ---------------------------------------------------------------------------
 // fp32 x and W through LDS DMA (K % 32 == 0, 16-byte aligned rows, each
-// operand under 2 GiB): the tile, fragment reads and MFMA order of
-// gemm_f32_kernel (so the same results), without staging every k-tile
-// through VGPRs and ds_write.  A buffer_load_dwordx4 ... lds writes 8 LDS
-// rows of 128 bytes; lane l fetches source chunk (l & 7) ^ (row & 7), which
-// lands at chunk position l & 7: the XOR swizzle the fragment reads expect.
-// Rows past M / N are clamped to the last valid row (their results are
-// never stored).  Two stages: the DMA of k-tile t + 1 is issued right after
-// the barrier that opens k-tile t, one k-tile of MFMAs ahead of its use.
+// operand under 2 GiB): the tile and fragment reads of gemm_f32_kernel,
+// without staging every k-tile through VGPRs and ds_write.  A
+// buffer_load_dwordx4 ... lds writes 64 lanes x 16 bytes of LDS rows; lane
+// l fetches the source chunk that the row's XOR swizzle puts at its
+// position, so the fragment reads need no other change.  Rows past M / N
+// are clamped to the last valid row (their results are never stored).  Two
+// stages: the DMA of k-tile t + 1 is issued right after the barrier that
+// opens k-tile t, one k-tile of MFMAs ahead of its use.
+// BK = 32 (64 KB of LDS, two workgroups per CU) keeps the MFMA order of
+// gemm_f32_kernel, so the same bits; the residual GEMMs use it (143 VGPRs
+// allow no more workgroups anyway).  BK = 16 (32 KB, 54 VGPRs: four per CU)
+// for the others: fp32 MelBandRoformer QKV 494 -> 467 us, FF1 472 -> 442 us;
+// the K pairs summed per MFMA differ, so the last bits do.
 // ---------------------------------------------------------------------------
-template <int BM, int BN, bool RES, typename OutT>
+template <int BM, int BN, int BK, bool RES, typename OutT>
 __global__ __launch_bounds__(kThreads) void gemm_f32_dma_kernel(
     const float* __restrict__ A, const float* __restrict__ W, const float* __restrict__ bias,
     const OutT* residual, OutT* out, int M, int N, int K, int act, int tiles_n, int per_xcd,
     int vec) {
-    constexpr int BK = 32;
+    static_assert(BK == 32 || BK == 16, "k-tile of 32 or 16 floats");
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int MI = WM / 32, NI = WN / 32;
-    constexpr int RPI = 8;                    // LDS rows per DMA instruction
+    constexpr int CPR = BK / 4;               // 16-byte chunks per LDS row
+    constexpr int RPI = 64 / CPR;             // LDS rows per DMA instruction
     constexpr int NWAVE = kThreads / 64;
     constexpr int A_INST = BM / RPI / NWAVE;  // per wave and k-tile
     constexpr int B_INST = BN / RPI / NWAVE;
@@ -350,19 +356,22 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_dma_kernel(
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wid >> 1, wn = wid & 1;
     const int lrow = lane & 31, lhalf = lane >> 5;
-    const int sub = lane >> 3, pch = lane & 7;
+    const int sub = lane / CPR, pch = lane % CPR;
+    // Chunk c of LDS row r sits at c ^ swz(r): 128-byte rows rotate by r, 64-byte rows by
+    // r / 4, so the 16 rows one b128 read pass touches fall in distinct banks.
+    auto swz = [](int r) { return CPR == 8 ? (r & 7) : ((r >> 2) & 3); };
 
     const int a_bytes = M * K * 4, b_bytes = N * K * 4;  // < 2^31 (checked on the host)
     uint32_t aoff[A_INST], boff[B_INST];
 #pragma unroll
     for (int i = 0; i < A_INST; ++i) {
         const int rl = (wid * A_INST + i) * RPI + sub;
-        aoff[i] = (uint32_t)(min(m0 + rl, M - 1) * K + ((pch ^ (rl & 7)) << 2)) * 4u;
+        aoff[i] = (uint32_t)(min(m0 + rl, M - 1) * K + ((pch ^ swz(rl)) << 2)) * 4u;
     }
 #pragma unroll
     for (int i = 0; i < B_INST; ++i) {
         const int rl = (wid * B_INST + i) * RPI + sub;
-        boff[i] = (uint32_t)(min(n0 + rl, N - 1) * K + ((pch ^ (rl & 7)) << 2)) * 4u;
+        boff[i] = (uint32_t)(min(n0 + rl, N - 1) * K + ((pch ^ swz(rl)) << 2)) * 4u;
     }
     auto issue = [&](int kt, int buf) {
         const uint32_t kb = (uint32_t)(kt * BK) * 4u;
@@ -393,18 +402,18 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_dma_kernel(
         const float* As = lds[cur];
         const float* Bs = lds[cur] + BM * BK;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int c = lhalf * 4 + t;
+        for (int t = 0; t < BK / 8; ++t) {
+            const int c = lhalf * (BK / 8) + t;
             f4 af[MI], bf[NI];
 #pragma unroll
             for (int i = 0; i < MI; ++i) {
                 int r = wm * WM + i * 32 + lrow;
-                af[i] = *reinterpret_cast<const f4*>(As + r * BK + ((c ^ (r & 7)) << 2));
+                af[i] = *reinterpret_cast<const f4*>(As + r * BK + ((c ^ swz(r)) << 2));
             }
 #pragma unroll
             for (int j = 0; j < NI; ++j) {
                 int r = wn * WN + j * 32 + lrow;
-                bf[j] = *reinterpret_cast<const f4*>(Bs + r * BK + ((c ^ (r & 7)) << 2));
+                bf[j] = *reinterpret_cast<const f4*>(Bs + r * BK + ((c ^ swz(r)) << 2));
             }
 #pragma unroll
             for (int s = 0; s < 4; ++s)
@@ -1220,10 +1229,10 @@ int launch_f32(const void* x, bool x_f16, const float* w, const float* bias,
         (int64_t)M * K * 4 < ((int64_t)1 << 31) && (int64_t)N * K * 4 < ((int64_t)1 << 31)) {
         const float* xf = reinterpret_cast<const float*>(x);
         if (res)
-            hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN, true, OutT>), dim3(grid), dim3(kThreads),
+            hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN, 32, true, OutT>), dim3(grid), dim3(kThreads),
                                0, s, xf, w, bias, res, out, M, N, K, act, tiles_n, per_xcd, vec);
         else
-            hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN, false, OutT>), dim3(grid), dim3(kThreads),
+            hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN, 16, false, OutT>), dim3(grid), dim3(kThreads),
                                0, s, xf, w, bias, res, out, M, N, K, act, tiles_n, per_xcd, vec);
         return check_launch("gemm_f32_dma_kernel");
     }
