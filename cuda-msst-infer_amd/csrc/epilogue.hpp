@@ -83,8 +83,10 @@ struct EpiRope {
 // for the padding; reads stay conflict-free, writes see at most two-way
 // conflicts.
 // NOBIAS: the accumulators already hold the bias (no add here).
+// UMAX: rows per lane and batch at most (fewer keep fewer residual rows in
+// flight, for kernels that need the registers).
 template <int MI, int NI, int IP, int EPI, typename OutT, bool TR = false, int ACT = -1,
-          bool SWZ = false, bool NOBIAS = false>
+          bool SWZ = false, bool NOBIAS = false, int UMAX = 8>
 __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds, int lane,
                                                int row0, int col0, int M, int N,
                                                const float* __restrict__ bias, int act,
@@ -100,7 +102,7 @@ __device__ __forceinline__ void store_tile_lds(f16x (&acc)[MI][NI], float* wlds,
     constexpr int LPR = WN / 4;    // lanes per row
     constexpr int RPI = 64 / LPR;  // rows per iteration
     constexpr int ITERS = IP * 32 / RPI;
-    constexpr int U = ITERS >= 8 ? 8 : ITERS;
+    constexpr int U = ITERS >= UMAX ? UMAX : ITERS;
     static_assert(ITERS % U == 0, "batch must divide the row count");
     constexpr int BPP = ITERS / U;        // batches per pass
     constexpr int NB = (MI / IP) * BPP;   // batches in total

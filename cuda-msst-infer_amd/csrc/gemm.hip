@@ -323,10 +323,11 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
 // are clamped to the last valid row (their results are never stored).  Two
 // stages: the DMA of k-tile t + 1 is issued right after the barrier that
 // opens k-tile t, one k-tile of MFMAs ahead of its use.
-// BK = 32 (64 KB of LDS, two workgroups per CU) keeps the MFMA order of
-// gemm_f32_kernel, so the same bits; the residual GEMMs use it (143 VGPRs
-// allow no more workgroups anyway).  BK = 16 (32 KB, 54 VGPRs: four per CU)
-// for the others: fp32 MelBandRoformer QKV 494 -> 467 us, FF1 472 -> 442 us;
+// BK = 32 (64 KB of LDS, two workgroups per CU) would keep the MFMA order
+// of gemm_f32_kernel and so its bits.  BK = 16 (32 KB) lets four workgroups
+// share a CU: 54 VGPRs, and 53 for the residual epilogue with 2 rows per
+// batch (143 with 8).  fp32 MelBandRoformer layer against BK = 32: QKV
+// 494 -> 467 us, FF1 472 -> 442, out-projection 190 -> 172, FF2 475 -> 450;
 // the K pairs summed per MFMA differ, so the last bits do.
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int BK, bool RES, typename OutT>
@@ -429,7 +430,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_dma_kernel(
     constexpr int kRegion = (int)(sizeof(lds) / sizeof(float) / 4);
     constexpr int kIP = pick_ip<MI, WN, kRegion>();
     static_assert(kIP * 32 * WN <= kRegion, "epilogue staging does not fit in LDS");
-    store_tile_lds<MI, NI, kIP, RES ? kEpiRes : kEpiPlain, OutT>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
+    store_tile_lds<MI, NI, kIP, RES ? kEpiRes : kEpiPlain, OutT, false, -1, false, false, RES ? 2 : 8>(acc, reinterpret_cast<float*>(&lds[0][0]) + wid * kRegion,
                                       lane, m0 + wm * WM, n0 + wn * WN, M, N, bias, act, residual,
                                       out, vec != 0);
 }
@@ -1229,7 +1230,7 @@ int launch_f32(const void* x, bool x_f16, const float* w, const float* bias,
         (int64_t)M * K * 4 < ((int64_t)1 << 31) && (int64_t)N * K * 4 < ((int64_t)1 << 31)) {
         const float* xf = reinterpret_cast<const float*>(x);
         if (res)
-            hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN, 32, true, OutT>), dim3(grid), dim3(kThreads),
+            hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN, 16, true, OutT>), dim3(grid), dim3(kThreads),
                                0, s, xf, w, bias, res, out, M, N, K, act, tiles_n, per_xcd, vec);
         else
             hipLaunchKernelGGL((gemm_f32_dma_kernel<BM, BN, 16, false, OutT>), dim3(grid), dim3(kThreads),
