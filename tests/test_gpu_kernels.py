@@ -196,6 +196,33 @@ def test_linear_residual_in_place(msst, oracle, cuda, wd):
     assert rel_err(host(xr), r) < tol(wd)
 
 
+# fp32 x and W with K % 32 == 0 take the LDS-DMA fp32 kernel (16-float k-tiles, rows past
+# M / N clamped to the last valid row); K = 40 takes the register-staged one.  Ragged M and
+# N (a column tile with two valid rows), one and several k-tiles, residual with an
+# activation, and a second call on fewer rows.
+F32_EDGE = [(1, 32, 17), (129, 32, 130), (257, 96, 200), (1000, 64, 129), (333, 40, 150)]
+
+
+@pytest.mark.parametrize("M,K,N", F32_EDGE)
+@pytest.mark.parametrize("act", ["none", "gelu", "sigmoid"])
+def test_linear_f32_edges(msst, oracle, cuda, M, K, N, act):
+    rng = np.random.default_rng(M * 7 + K * 3 + N)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    b = (rng.standard_normal(N) * 0.05).astype(np.float32)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    xd, wd = dev(x), dev(w)
+    y = msst.linear(xd, wd, dev(b), act, out_dtype=torch.float32)
+    assert rel_err(host(y), oracle.linear(x, w, b, act)) < TOL_F32
+    xr = dev(res)
+    msst.linear(xd, wd, dev(b), act, residual=xr, out=xr)
+    assert rel_err(host(xr), oracle.linear(x, w, b, act, residual=res)) < TOL_F32
+    M2 = max(1, M // 2)
+    xr2 = dev(res[:M2])
+    msst.linear(xd[:M2], wd, dev(b), act, residual=xr2, out=xr2)
+    assert rel_err(host(xr2), oracle.linear(x[:M2], w, b, act, residual=res[:M2])) < TOL_F32
+
+
 SWEEP_KN = [(384, 1536), (1536, 384), (512, 1536), (512, 2048), (2048, 512), (384, 8), (512, 8),
             (512, 384), (512, 512)]
 
