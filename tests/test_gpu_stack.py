@@ -176,3 +176,39 @@ def test_full_depth_properties(msst, cuda, name, F, dim, ff, depth, mbr):
     assert torch.equal(again, singles[0])
     # the stack changed the input substantially (it is not an identity)
     assert (y4 - x).abs().max().item() > 0.1
+
+
+@pytest.mark.parametrize("fp16", [True, False])
+def test_stack_graph_capture_replays(msst, cuda, fp16):
+    """The stack launches kernels only (no allocation, memset or host
+    synchronisation), so a caller can capture it in a HIP graph.  Every replay,
+    with eager stack work and synchronisations between them, must equal the
+    eager result bit for bit (full-size BSRoformer chunk, depth 2)."""
+    T, F, dim, heads, ff, depth = 801, 62, 512, 8, 2048, 2
+    layers = make_layers(11, 2 * depth, dim, heads, ff, fp16, final_norm=False)
+    rng = np.random.default_rng(12)
+    fg = (1 + rng.standard_normal(dim) * 0.02).astype(np.float32)
+    x0 = torch.from_numpy(rng.standard_normal((1, T, F, dim)).astype(np.float32)).cuda()
+    st = build_stack(msst, layers, fp16, 1, T, F, dim, heads, ff, fg)
+    ref = st(x0.clone())
+    torch.cuda.synchronize()
+    xg = x0.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        st(xg)  # first launch of every kernel outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st(xg)
+    torch.cuda.synchronize()
+    other = x0.clone()
+    for _ in range(3):
+        xg.copy_(x0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(xg, ref)
+        st(other)  # eager work between replays
+        torch.cuda.synchronize()
