@@ -56,6 +56,36 @@ def test_stack_noalloc_matches_workspace_entry(msst, order):
         assert torch.equal(got, ref), float((got - ref).abs().max())
 
 
+def test_stack_noalloc_graph_capture(msst):
+    """The callers this entry point is for include code under HIP graph
+    capture: a captured call replays three times, with eager calls of both
+    entry points between the replays, each bit-identical to the workspace
+    entry point."""
+    st, x = _stack(msst, 14, 1, 161, 62, 512, 2, 2048, False)
+    ref = x.clone()
+    st(ref)
+    xg = x.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        st.call_noalloc(xg)  # first launches outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st.call_noalloc(xg)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        xg.copy_(x)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(xg, ref), float((xg - ref).abs().max())
+        st(x.clone())
+        st.call_noalloc(x.clone())
+        torch.cuda.synchronize()
+
+
 def test_stack_noalloc_rejects_oversized_stack(msst):
     st, x = _stack(msst, 13, 1, 801, 62, 512, 1, 2048, False)  # ~307 MB of workspace
     assert msst.lib().msst_roformer_stack_workspace(st.desc) > msst.STACK_SCRATCH_BYTES
