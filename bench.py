@@ -187,7 +187,7 @@ def host_cpu_model():
 
 
 def batch4_stack(msst, torch, layers, final_gamma, steps):
-    """Config 5: four overlapped 8 s chunks in one step (time layers on
+    """Four overlapped 8 s chunks in one step (time layers on
     [248, 801, 512], frequency layers on [3204, 62, 512], M = 198648);
     ms per chunk = step time / 4, and the GEMM replay at the same M."""
     B = 4
@@ -213,7 +213,7 @@ def batch4_stack(msst, torch, layers, final_gamma, steps):
 
 
 def gemm_sweep(msst, torch):
-    """Config 2: every (M, K, N, epilogue, dtype) of the sweep, each GEMM
+    """Every (M, K, N, epilogue, dtype) of the GEMM sweep, each GEMM
     HIP-event timed alone (10 launches after one warm-up).  fp16: x, W fp16,
     fp32 accumulation, fp16 out; fp32: x, W, out fp32 (true fp32 MFMA).
     Bias ~ N(0, 0.02), A ~ N(0, 1), W ~ N(0, 0.02).  MFMA-bound shapes
@@ -254,8 +254,8 @@ def gemm_sweep(msst, torch):
     return out
 
 
-def config1_fp32_layer(msst, torch):
-    """Config 1 on the GPU: one MelBandRoformer time layer in fp32 on
+def fp32_mbr_time_layer(msst, torch):
+    """On the GPU: one MelBandRoformer time layer in fp32 on
     x [60, 801, 384] (fp32 weights ~ N(0, 0.02), true fp32 MFMA), the whole
     layer HIP-event timed, and each fp32 kernel alone against the fp32
     matrix peak (the attention's QK^T + PV flops as MFMA work)."""
@@ -523,7 +523,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--batch", type=int, default=1, help="chunks per step (config 5 uses 4)")
+    ap.add_argument("--batch", type=int, default=1, help="chunks per step (the batch-of-4 report uses 4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other configurations' sections (batch of 4 chunks, fp32 "
@@ -535,7 +535,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(chunk-level data parallelism across GPUs is described in DESIGN.md).",
+              "(chunks are independent: several GPUs would each run their own chunks).",
               file=sys.stderr)
         sys.exit(2)
 
@@ -645,7 +645,7 @@ def main():
     if not args.no_configs:
         out["config5_batch4"] = batch4_stack(msst, torch, layers, final_gamma,
                                              max(2, min(5, args.steps)))
-        out["config1_fp32_layer"] = config1_fp32_layer(msst, torch)
+        out["config1_fp32_layer"] = fp32_mbr_time_layer(msst, torch)
         out["config2_gemm_sweep"] = gemm_sweep(msst, torch)
     if not args.no_cpu:
         cpu, parity = cpu_baseline_and_parity(msst, torch, args)

@@ -230,8 +230,9 @@ SWEEP_KN = [(384, 1536), (1536, 384), (512, 1536), (512, 2048), (2048, 512), (38
 @pytest.mark.parametrize("M", [48060, 49662, 198648])
 @pytest.mark.parametrize("K,N", SWEEP_KN)
 @pytest.mark.parametrize("wd", ["f16", "f32"])
-def test_linear_baseline_sweep(msst, oracle, cuda, M, K, N, wd):
-    """The BASELINE GEMM sweep shapes, all three epilogues, checked on a
+def test_linear_shape_sweep(msst, oracle, cuda, M, K, N, wd):
+    """The benchmark's GEMM sweep shapes (Roformer linears at the chunk token
+    counts of one and four chunks), all three epilogues, checked on a
     sample of rows (every output row depends only on its own input row, so
     the sample check is exact parity on those rows)."""
     g = torch.Generator(device="cuda").manual_seed(M + K * 7 + N)

@@ -1,13 +1,16 @@
 """Layer- and stack-level parity of the HIP Roformer path against the CPU
-oracle, at the BASELINE configurations.
+oracle, on the workloads the benchmark reports:
 
-  config 1  MelBandRoformer time layer, fp32, x [60, 801, 384]      (full size)
-  config 3  MelBandRoformer stack, fp16, dim 384, [60 bands, 801]   (depth 1 and
-            the full depth 6 at full size vs the oracle; properties)
-  config 4  BSRoformer stack, fp16, dim 512, [62 bands, 801]        (depth 1 and
-            the full depth 12 at full size vs the oracle; properties)
-  config 5  BSRoformer, batch of 4 chunks                           (batch
-            consistency: bit-identical to 4 single-chunk runs)
+  MelBandRoformer time layer, fp32, x [60, 801, 384]      (full size)
+  MelBandRoformer stack, fp16, dim 384, [60 bands, 801]   (depth 1 and the full
+                                                          depth 6 at full size vs
+                                                          the oracle; properties)
+  BSRoformer stack, fp16, dim 512, [62 bands, 801]        (depth 1 and the full
+                                                          depth 12 at full size vs
+                                                          the oracle; properties)
+  BSRoformer, batch of 4 chunks                           (batch consistency:
+                                                          bit-identical to 4
+                                                          single-chunk runs)
 Weights: matrices and biases ~ N(0, 0.02), gammas 1 + N(0, 0.02), x ~ N(0,1).
 """
 from __future__ import annotations
@@ -81,7 +84,7 @@ def test_stack_small(msst, oracle, cuda, B, T, F, dim, heads, ff, depth, fp16, m
     assert e < (TOL_F16 if fp16 else TOL_F32), e
 
 
-def test_config1_mbr_time_layer_fp32(msst, oracle, cuda):
+def test_mbr_time_layer_fp32_full_size(msst, oracle, cuda):
     """Single MelBandRoformer time layer, fp32, x [60, 801, 384], N(0,1)."""
     F, T, dim, heads, ff = 60, 801, 384, 8, 1536
     layers = make_layers(0, 2, dim, heads, ff, False, final_norm=False)
@@ -99,7 +102,7 @@ def test_config1_mbr_time_layer_fp32(msst, oracle, cuda):
 @pytest.mark.parametrize("name,F,dim,ff,mbr", [("bsr", 62, 512, 2048, False),
                                                ("mbr", 60, 384, 1536, True)])
 def test_full_size_depth1_fp16(msst, oracle, cuda, name, F, dim, ff, mbr):
-    """Configs 3/4 at full spatial size, one depth (time + freq layer)."""
+    """Both stacks at full spatial size, one depth (time + freq layer)."""
     e = run_stack(msst, oracle, 1, 801, F, dim, 8, ff, 1, True, mbr, seed=4)
     assert e < TOL_F16, e
 
@@ -156,8 +159,8 @@ def test_stack_layer_schedule_against_oracle(msst, oracle, cuda, fp16, mbr):
 @pytest.mark.parametrize("name,F,dim,ff,depth,mbr", [("bsr", 62, 512, 2048, 12, False),
                                                      ("mbr", 60, 384, 1536, 6, True)])
 def test_full_depth_properties(msst, cuda, name, F, dim, ff, depth, mbr):
-    """Configs 3/4 at full depth: finite, deterministic, and the batch-of-4
-    run (config 5 for BSR) equals four single-chunk runs bit for bit — every
+    """Both stacks at full depth: finite, deterministic, and the batch-of-4
+    run equals four single-chunk runs bit for bit — every
     kernel's per-row / per-sequence arithmetic is independent of the batch."""
     T, heads = 801, 8
     layers = make_layers(5, 2 * depth, dim, heads, ff, True, final_norm=mbr)
